@@ -1,0 +1,250 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X int4-dequant GEMV/GEMM (libspaceslug_runtime.so, gfx950).
+
+Headline (value): decode GEMV, M=1, K=4096, N=14336, int4 group-32 weights, 64
+distinct weight copies (2.35 GB, far beyond the 256 MB last-level cache) resident
+in HBM and swept in turn. One step = one sweep = 64 GEMV launches through the
+C-ABI device entry point spaceslug_q4gemm_device on torch's current stream.
+value = algorithmic bytes of all timed launches / timed wall time on the GPU
+(HIP events around the timed region, on the launch stream).
+
+Algorithmic bytes per launch (each tensor once): packed nibbles K*N/2 + fp32
+scales 4*N*K/32 + x 4*M*K + y 4*M*N. Flops per launch: 2*M*N*K.
+
+Also reported in the same JSON line:
+  - "roofline": achieved GB/s of the GEMV kernel vs MI355X's 8 TB/s HBM peak;
+  - "prefill": the M=2048, K=4096, N=14336 GEMM in TFLOP/s vs the 157.3 TFLOP/s
+    fp32 MFMA peak (the second half of the headline metric);
+  - "small_batch" (M=16, K=N=4096, 32 weight copies per step) and "lora"
+    (M=512, K=N=4096, rank 16) throughput;
+  - "cpu_baseline": the C CPU oracle (double-precision restatement of the
+    reference's cpu_reference) on a bounded sample of the same GEMV workload,
+    timed on this host's cores.
+Inputs are synthetic (torch RNG on the GPU: N(0,1) activations, uniform
+nibbles in [-8, 7], scales uniform in [0.01, 0.05]).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "spaceslug-main_amd"))
+sys.path.insert(0, str(REPO))
+
+METRIC = "int4 GEMV GB/s @M=1 & GEMM TFLOP/s @M=2048, % of MI355X roofline"
+HBM_PEAK_GBS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+
+def algo_bytes(m: int, n: int, k: int, rank: int = 0) -> int:
+    b = n * k // 2 + 4 * n * (k // 32) + 4 * m * k + 4 * m * n
+    if rank:
+        b += 4 * k * rank + 4 * rank * n
+    return b
+
+
+def algo_flops(m: int, n: int, k: int, rank: int = 0) -> int:
+    f = 2 * m * n * k
+    if rank:
+        f += 2 * m * rank * (k + n)
+    return f
+
+
+def make_weights(torch, n: int, k: int, copies: int, gen):
+    packed = [torch.randint(0, 256, (n, k // 2), dtype=torch.uint8, device="cuda", generator=gen) for _ in range(copies)]
+    scales = [torch.rand((n, k // 32), dtype=torch.float32, device="cuda", generator=gen) * 0.04 + 0.01
+              for _ in range(copies)]
+    return packed, scales
+
+
+def time_region(torch, fn, steps: int, warmup: int) -> float:
+    """Runs fn() warmup times untimed, then steps times between HIP events; returns ms per step."""
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
+def bench_gemv(torch, session, steps: int, warmup: int, copies: int = 64, use_graph: bool = False) -> dict:
+    m, n, k = 1, 14336, 4096
+    gen = torch.Generator(device="cuda").manual_seed(1234)
+    packed, scales = make_weights(torch, n, k, copies, gen)
+    x = torch.randn((m, k), dtype=torch.float32, device="cuda", generator=gen)
+    ys = [torch.empty((m, n), dtype=torch.float32, device="cuda") for _ in range(copies)]
+
+    def sweep():
+        st = torch.cuda.current_stream().cuda_stream
+        for i in range(copies):
+            session.q4gemm_device(x.data_ptr(), packed[i].data_ptr(), scales[i].data_ptr(), ys[i].data_ptr(), m, n,
+                                  k, st)
+
+    fn = sweep
+    if use_graph:
+        sweep()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            sweep()
+        fn = g.replay
+    ms = time_region(torch, fn, steps, warmup)
+    per_launch_s = ms * 1e-3 / copies
+    bytes_per = algo_bytes(m, n, k)
+    gbs = bytes_per / per_launch_s / 1e9
+    return {"ms_per_step": ms, "per_launch_us": per_launch_s * 1e6, "gbs": gbs, "bytes_per_launch": bytes_per,
+            "copies": copies, "graph": use_graph,
+            "tflops": algo_flops(m, n, k) / per_launch_s / 1e12}
+
+
+def bench_gemm(torch, session, m: int, n: int, k: int, copies: int, steps: int, warmup: int, rank: int = 0) -> dict:
+    gen = torch.Generator(device="cuda").manual_seed(99)
+    packed, scales = make_weights(torch, n, k, copies, gen)
+    x = torch.randn((m, k), dtype=torch.float32, device="cuda", generator=gen)
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    if rank:
+        la = torch.randn((k, rank), dtype=torch.float32, device="cuda", generator=gen) * 0.02
+        lb = torch.randn((rank, n), dtype=torch.float32, device="cuda", generator=gen) * 0.02
+
+    def step():
+        st = torch.cuda.current_stream().cuda_stream
+        for i in range(copies):
+            if rank:
+                session.q4gemm_lora_device(x.data_ptr(), packed[i].data_ptr(), scales[i].data_ptr(), la.data_ptr(),
+                                           lb.data_ptr(), y.data_ptr(), m, n, k, rank, 32.0 / rank, st)
+            else:
+                session.q4gemm_device(x.data_ptr(), packed[i].data_ptr(), scales[i].data_ptr(), y.data_ptr(), m, n, k,
+                                      st)
+
+    ms = time_region(torch, step, steps, warmup)
+    per_call = ms * 1e-3 / copies
+    fl = algo_flops(m, n, k, rank)
+    by = algo_bytes(m, n, k, rank)
+    tf = fl / per_call / 1e12
+    return {"m": m, "n": n, "k": k, "rank": rank, "copies": copies, "ms_per_call": per_call * 1e3,
+            "tflops": tf, "gbs": by / per_call / 1e9, "flops_per_call": fl, "bytes_per_call": by,
+            "roofline": {"bound": "mfma", "achieved": tf, "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": tf / FP32_MFMA_PEAK_TFLOPS}}
+
+
+def cpu_baseline(budget_s: float) -> dict:
+    """Times the C oracle (double, from the packed bytes) on whole GEMV calls of the same shape."""
+    import numpy as np
+
+    from oracle import oracle as o
+
+    m, n, k = 1, 14336, 4096
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    threads = max(1, min(threads, os.cpu_count() or 1))
+    rng = np.random.default_rng(7)
+    calls = 0
+    elapsed = 0.0
+    while elapsed < budget_s or calls < 2:
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        packed = rng.integers(0, 256, size=(n, k // 2), dtype=np.uint8)
+        scales = (rng.random((n, k // 32), dtype=np.float32) * 0.04 + 0.01).astype(np.float32)
+        t0 = time.perf_counter()
+        o.q4gemm_packed(x, packed, scales, threads=threads)
+        elapsed += time.perf_counter() - t0
+        calls += 1
+    gbs = algo_bytes(m, n, k) * calls / elapsed / 1e9
+    return {"value": gbs, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{calls} GEMV calls M=1 K=4096 N=14336 (distinct random weights), double-precision C oracle "
+                      f"over {threads} OpenMP threads, {elapsed:.1f} s"}
+
+
+def load_traffic() -> float | None:
+    p = REPO / "profiles" / "q4_gemv_m1_k4096_n14336_traffic.json"
+    if p.is_file():
+        try:
+            return float(json.loads(p.read_text())["hbm_bytes_per_launch"])
+        except Exception:
+            return None
+    return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--graph", action="store_true", help="replay the 64-launch sweep as one HIP graph")
+    ap.add_argument("--gemv-only", action="store_true", help="skip the secondary GEMM configurations")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget (0 disables)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the int4 path is measured "
+              f"on a single MI355X", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    from spaceslug_amd import BackendSession
+
+    session = BackendSession()
+    session.capability()  # fails loudly when the HIP library is missing
+
+    print(f"[bench] gemv sweep steps={args.steps} warmup={args.warmup} graph={args.graph}", file=sys.stderr,
+          flush=True)
+    gemv = bench_gemv(torch, session, args.steps, args.warmup, use_graph=args.graph)
+    result = {
+        "metric": METRIC,
+        "value": round(gemv["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(gemv["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "int4 group-32 decode GEMV M=1 K=4096 N=14336, 64 weight copies swept per step",
+                   "m": 1, "k": 4096, "n": 14336, "copies": 64, "launch": "hip-graph" if args.graph else "stream",
+                   "parallelism": "single-gpu"},
+        "roofline": {"bound": "hbm", "achieved": round(gemv["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gemv["gbs"] / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
+                     "bytes_per_launch": gemv["bytes_per_launch"],
+                     "avg_launch_us": round(gemv["per_launch_us"], 3)},
+    }
+    del gemv
+    torch.cuda.empty_cache()
+    if not args.gemv_only:
+        print("[bench] prefill 2048x4096x14336", file=sys.stderr, flush=True)
+        pre = bench_gemm(torch, session, 2048, 14336, 4096, copies=1, steps=max(3, args.steps // 10), warmup=2)
+        result["prefill"] = {"value": round(pre["tflops"], 3), "unit": "TFLOP/s",
+                             "ms_per_call": round(pre["ms_per_call"], 4), "roofline": pre["roofline"]}
+        torch.cuda.empty_cache()
+        print("[bench] small batch 16x4096x4096 x32 copies", file=sys.stderr, flush=True)
+        sb = bench_gemm(torch, session, 16, 4096, 4096, copies=32, steps=max(3, args.steps // 5), warmup=2)
+        result["small_batch"] = {"value": round(sb["tflops"], 3), "unit": "TFLOP/s", "gbs": round(sb["gbs"], 2),
+                                 "us_per_call": round(sb["ms_per_call"] * 1e3, 3), "roofline": sb["roofline"]}
+        torch.cuda.empty_cache()
+        print("[bench] lora 512x4096x4096 r16", file=sys.stderr, flush=True)
+        lo = bench_gemm(torch, session, 512, 4096, 4096, copies=1, steps=max(3, args.steps // 5), warmup=2, rank=16)
+        result["lora"] = {"value": round(lo["tflops"], 3), "unit": "TFLOP/s",
+                          "us_per_call": round(lo["ms_per_call"] * 1e3, 3), "roofline": lo["roofline"]}
+    if args.cpu_seconds > 0:
+        print("[bench] cpu baseline", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,128 @@
+/*
+ * Spaceslug runtime C-ABI, MI355X (gfx950) native build.
+ *
+ * Drop-in superset of the reference's top-level C-ABI (native/runtime_abi.h:1-9)
+ * and of the two symbols the reference's Python host binds unconditionally
+ * (python/spaceslug/backend.py:62-67): spaceslug_vector_add and spaceslug_sgemm.
+ * Everything else is the int4-dequant GEMM/GEMV the reference implements as the
+ * Vulkan shader vulkan-runtime/shaders/q4gemm.comp, which has no C-ABI export in
+ * the reference; its entry points below follow the export conventions of
+ * vulkan-runtime/src/api/sgemm_api.h:7-9 and lora_delta_api.h:5-13.
+ *
+ * Conventions (reference: sgemm_api.cpp:38,63; lora_delta_api.h:7;
+ * tiny_forward_persistent.h:270,312,474,556-558):
+ *   - C linkage, plain pointers, uint32_t dimensions, int status.
+ *   - 0 = success; 1 = invalid arguments (null pointer, zero or unsupported
+ *     dimension, misaligned device pointer); 2 = device/runtime failure caught at
+ *     the boundary (including "no HIP device"); -4 = capability not supported.
+ *     No C++ exception crosses the boundary.
+ *   - Host-pointer entry points are synchronous: inputs are copied to the GPU and
+ *     the output is fully written before return. The caller owns every buffer.
+ *   - *_device entry points take device pointers and a hipStream_t (passed as
+ *     void*; NULL = the default stream) and only enqueue work: outputs are valid
+ *     once the stream is synchronised.
+ *   - Persistent state lives behind opaque handles: create returns NULL on
+ *     failure, destroy accepts NULL.
+ *   - Single-threaded per process like the reference (its exec engine is
+ *     documented single-threaded, engine.h:37): concurrent calls from several
+ *     host threads are not supported.
+ *
+ * Weight format (q4gemm.comp:7-19; test_q4gemm.cpp:7-17), group size fixed at 32:
+ *   logical W is K x N, each value v in [-8, 7]; stored as the nibble v & 0xF.
+ *   w_packed is uint8[N][K/2]: byte n*(K/2) + k/2 holds k even in bits 0..3 and
+ *   k odd in bits 4..7 (byte-identical to the reference's little-endian uint32
+ *   words). w_scales is float[N][K/32]; dequant(k, n) = v(k, n) * w_scales[n*(K/32) + k/32].
+ *   x is float[M][K] row-major; y is float[M][N] row-major.
+ *   y[m][n] = sum_k x[m][k] * dequant(k, n)   (fp32 inputs, fp32 output).
+ */
+#ifndef SPACESLUG_RUNTIME_ABI_H
+#define SPACESLUG_RUNTIME_ABI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SPACESLUG_OK 0
+#define SPACESLUG_ERR_INVALID 1
+#define SPACESLUG_ERR_DEVICE 2
+#define SPACESLUG_ERR_UNSUPPORTED (-4)
+
+/* Largest LoRA rank the fused epilogue accepts. */
+#define SPACESLUG_Q4_MAX_LORA_RANK 64u
+
+/* native/runtime_abi.h:6 (CPU implementation native/runtime_abi.cpp:3-7):
+ * output[i] = left[i] + right[i]. Returns 1 on a null pointer, else 0. */
+int spaceslug_vector_add(const float* left, const float* right, float* output, size_t count);
+
+/* vulkan-runtime/src/api/sgemm_api.h:7-9 (implementation sgemm_api.cpp:37-63):
+ * fp32 row-major C[m][n] = A[m][k] * B[k][n] on the GPU. Same shape contract as
+ * the reference: m % 64 == 0, n % 64 == 0, k % 32 == 0, all nonzero, else 1.
+ * *max_relative_error is written as 0, as the reference does. Synchronous. */
+int spaceslug_sgemm(const float* a, const float* b, float* c, uint32_t m, uint32_t n, uint32_t k,
+                    float* max_relative_error);
+
+/* Capability string of the int4 path (pattern: tiny_forward_persistent.h:557-558).
+ * Static storage, never NULL. */
+const char* spaceslug_q4gemm_capability(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* spaceslug_last_error(void);
+
+/* Replaces q4gemm.comp:61-175 as dispatched by test_q4gemm.cpp:335-356, as a
+ * C-ABI call: synchronous host pointers, any m >= 1 and n >= 1, k % 32 == 0
+ * (the reference shader additionally needs m % 64 == 0 and n % 64 == 0,
+ * q4gemm.comp:36-37). */
+int spaceslug_q4gemm(const float* x, const uint8_t* w_packed, const float* w_scales, float* y,
+                     uint32_t m, uint32_t n, uint32_t k);
+
+/* Int4 projection with a fused LoRA epilogue, replacing the three-call composition
+ * of backend.py:794-799 (spaceslug_sgemm, spaceslug_lora_delta with B pre-scaled
+ * by alpha/rank, then a host add; lora_delta_api.h:5-13, lora.py:21-23):
+ *   y = x * dequant(W) + scale * (x * lora_a) * lora_b
+ * lora_a is float[k][rank], lora_b is float[rank][n], both row-major (the layouts
+ * of lora_delta.comp:2). scale is alpha / rank. 1 <= rank <= SPACESLUG_Q4_MAX_LORA_RANK.
+ * Synchronous host pointers. */
+int spaceslug_q4gemm_lora(const float* x, const uint8_t* w_packed, const float* w_scales,
+                          const float* lora_a, const float* lora_b, float* y,
+                          uint32_t m, uint32_t n, uint32_t k, uint32_t rank, float scale);
+
+/* Device-pointer, stream-ordered variant of spaceslug_q4gemm (no reference
+ * counterpart: the reference never passes device memory across its ABI).
+ * d_x, d_w_packed must be 16-byte aligned; d_w_scales, d_y 4-byte aligned.
+ * Enqueues only. The m <= 4 decode path uses no device memory beyond its
+ * arguments; the MFMA path, when it splits K across workgroups, keeps its
+ * partial sums in a library-owned device workspace that is allocated on first
+ * use and grown on demand (growth synchronises the device, steady state does
+ * not allocate). Calls that share a device share that workspace, so they must
+ * not overlap (same single-threaded rule as above). */
+int spaceslug_q4gemm_device(const float* d_x, const uint8_t* d_w_packed, const float* d_w_scales,
+                            float* d_y, uint32_t m, uint32_t n, uint32_t k, void* stream);
+
+/* Device-pointer, stream-ordered variant of spaceslug_q4gemm_lora. Keeps
+ * T = x * lora_a (m * rank floats) and any K-split partials in the same
+ * library-owned device workspace as spaceslug_q4gemm_device. */
+int spaceslug_q4gemm_lora_device(const float* d_x, const uint8_t* d_w_packed,
+                                 const float* d_w_scales, const float* d_lora_a,
+                                 const float* d_lora_b, float* d_y, uint32_t m, uint32_t n,
+                                 uint32_t k, uint32_t rank, float scale, void* stream);
+
+/* Device-resident weights (handle pattern of tiny_forward_persistent.h:556 and
+ * .cpp:4751-4800, 5373-5378): uploads w_packed/w_scales once so repeated
+ * projections (backend.py:1719-1735 issues five per token) do not re-stage them. */
+typedef struct spaceslug_q4_weight spaceslug_q4_weight;
+
+spaceslug_q4_weight* spaceslug_q4_weight_create(const uint8_t* w_packed, const float* w_scales,
+                                                uint32_t n, uint32_t k);
+void spaceslug_q4_weight_destroy(spaceslug_q4_weight* weight);
+
+/* Synchronous host x/y against a weight handle: y[m][n] = x[m][k] * dequant(W). */
+int spaceslug_q4gemm_run(const spaceslug_q4_weight* weight, const float* x, float* y, uint32_t m);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

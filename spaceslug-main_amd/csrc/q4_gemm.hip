@@ -1,0 +1,349 @@
+// fp32-MFMA int4 GEMM for 5+ rows (prefill, small-batch decode, LoRA projections).
+//
+// Replaces q4gemm.comp:61-175 (64x64 tile, LDS-staged dequantised B, 4x4 FMA
+// micro-tile per thread) with a CDNA4 design built on v_mfma_f32_16x16x4_f32:
+//   - a wavefront owns a (16*WM) x (16*WN) output block, WM x WN MFMA tiles;
+//   - per 32-value scale group, lane (j = l%16, q = l/16) feeds the MFMA K slot
+//     q with k = 8q + t at step t = 0..7, so its B operands for column j are
+//     the 8 nibbles of ONE 32-bit word of the packed column (word q of the
+//     group's 16 bytes) and its A operands are 8 consecutive floats of row j
+//     (two 128-bit loads). Weights are decoded in registers (v_bfe_i32 +
+//     v_cvt_f32_i32, exact small integers) straight into the MFMA operand;
+//   - the MFMA accumulates P = x * v over one group (8 steps) in fp32 from
+//     zero, and the group is folded into a float64 accumulator as
+//     acc += (double)s * P. Scale application moves out of the inner loop, and
+//     the long K sum is carried in double, which keeps the max relative error
+//     against the double-precision reference well under 1e-5 at K = 4096;
+//   - operands of group g+1 are loaded while group g computes (register
+//     double buffering); A rows and weight columns go global -> VGPR through
+//     L1/L2 with no LDS round trip;
+//   - large grids are XCD-aware: workgroup ids are remapped so each of the 8
+//     XCDs (one L2 each) walks a contiguous band of output tiles, sharing A
+//     rows and weight columns within its L2;
+//   - when the grid is too small to fill 256 CUs, K is split across
+//     blockIdx.z and a second kernel sums the partials in a fixed order.
+// The fused LoRA epilogue adds scale * T[rows] * lb[:, cols] with T = x * la
+// precomputed by lora_t_kernel, using the same MFMA tile layout (r in the K slot).
+#include "q4_device.hpp"
+#include "q4_kernels.hpp"
+
+namespace spaceslug {
+namespace {
+
+template <int WM, int WN, int WAVES_M, int WAVES_N>
+struct TileShape {
+    static constexpr int kWaves = WAVES_M * WAVES_N;
+    static constexpr int kThreads = 64 * kWaves;
+    static constexpr int kBM = 16 * WM * WAVES_M;
+    static constexpr int kBN = 16 * WN * WAVES_N;
+};
+
+// Maps the linear workgroup id to (tile_n, tile_m) so that consecutive ids on
+// one XCD (hardware dispatches workgroup i to XCD i % 8) cover a contiguous
+// run of tiles, walked M-fastest inside column bands.
+__device__ __forceinline__ void xcd_tile(int tiles_m, int tiles_n, int& tm, int& tn) {
+    const int total = tiles_m * tiles_n;
+    const int id = blockIdx.x;
+    int lin = id;
+    if (total >= 64 && (total & 7) == 0) {
+        const int per_xcd = total >> 3;
+        lin = (id & 7) * per_xcd + (id >> 3);
+    }
+    tm = lin % tiles_m;
+    tn = lin / tiles_m;
+}
+
+template <int WM, int WN, int WAVES_M, int WAVES_N>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void q4_gemm_mfma_kernel(
+    const float* __restrict__ x, const uint32_t* __restrict__ wq, const float* __restrict__ ws,
+    float* __restrict__ out, int M, int N, int K, int tiles_m, int tiles_n, int groups_per_split,
+    const float* __restrict__ lt, const float* __restrict__ lb, int R, float lscale) {
+    using Shape = TileShape<WM, WN, WAVES_M, WAVES_N>;
+    const int lane = threadIdx.x & 63;
+    const int wid = threadIdx.x >> 6;
+    const int wm = wid % WAVES_M;
+    const int wn = wid / WAVES_M;
+    const int j = lane & 15;
+    const int q = lane >> 4;
+    const int G = K >> 5;
+
+    int tile_m, tile_n;
+    xcd_tile(tiles_m, tiles_n, tile_m, tile_n);
+    const int m0 = tile_m * Shape::kBM + wm * 16 * WM;
+    const int n0 = tile_n * Shape::kBN + wn * 16 * WN;
+    const int g_begin = blockIdx.y * groups_per_split;
+    const int g_end = min(G, g_begin + groups_per_split);
+
+    const float* arow[WM];
+#pragma unroll
+    for (int tm = 0; tm < WM; ++tm) {
+        const int row = min(m0 + 16 * tm + j, M - 1);
+        arow[tm] = x + static_cast<size_t>(row) * K + 8 * q;
+    }
+    const uint32_t* bcol[WN];
+    const float* scol[WN];
+#pragma unroll
+    for (int tn = 0; tn < WN; ++tn) {
+        const int col = min(n0 + 16 * tn + j, N - 1);
+        bcol[tn] = wq + static_cast<size_t>(col) * (K >> 3) + q;
+        scol[tn] = ws + static_cast<size_t>(col) * G;
+    }
+
+    double acc[WM][WN][4];
+#pragma unroll
+    for (int tm = 0; tm < WM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < WN; ++tn)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[tm][tn][i] = 0.0;
+
+    float4 alo[WM], ahi[WM];
+    uint32_t bw[WN];
+    float bs[WN];
+    if (g_begin < g_end) {
+#pragma unroll
+        for (int tm = 0; tm < WM; ++tm) {
+            alo[tm] = *reinterpret_cast<const float4*>(arow[tm] + g_begin * 32);
+            ahi[tm] = *reinterpret_cast<const float4*>(arow[tm] + g_begin * 32 + 4);
+        }
+#pragma unroll
+        for (int tn = 0; tn < WN; ++tn) {
+            bw[tn] = bcol[tn][g_begin * 4];
+            bs[tn] = scol[tn][g_begin];
+        }
+    }
+
+    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int g = g_begin; g < g_end; ++g) {
+        const int gn = min(g + 1, g_end - 1);
+        float4 alo_n[WM], ahi_n[WM];
+        uint32_t bw_n[WN];
+        float bs_n[WN];
+#pragma unroll
+        for (int tm = 0; tm < WM; ++tm) {
+            alo_n[tm] = *reinterpret_cast<const float4*>(arow[tm] + gn * 32);
+            ahi_n[tm] = *reinterpret_cast<const float4*>(arow[tm] + gn * 32 + 4);
+        }
+#pragma unroll
+        for (int tn = 0; tn < WN; ++tn) {
+            bw_n[tn] = bcol[tn][gn * 4];
+            bs_n[tn] = scol[tn][gn];
+        }
+
+        f32x4 P[WM][WN];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            float bv[WN];
+#pragma unroll
+            for (int tn = 0; tn < WN; ++tn) bv[tn] = nibble_signed(bw[tn], t);
+#pragma unroll
+            for (int tm = 0; tm < WM; ++tm) {
+                const float av = t == 0 ? alo[tm].x : t == 1 ? alo[tm].y : t == 2 ? alo[tm].z
+                               : t == 3 ? alo[tm].w : t == 4 ? ahi[tm].x : t == 5 ? ahi[tm].y
+                               : t == 6 ? ahi[tm].z : ahi[tm].w;
+#pragma unroll
+                for (int tn = 0; tn < WN; ++tn)
+                    P[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[tn], t == 0 ? zero : P[tm][tn], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int tn = 0; tn < WN; ++tn) {
+            const double s = static_cast<double>(bs[tn]);
+#pragma unroll
+            for (int tm = 0; tm < WM; ++tm)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[tm][tn][i] = fma(s, static_cast<double>(P[tm][tn][i]), acc[tm][tn][i]);
+        }
+#pragma unroll
+        for (int tm = 0; tm < WM; ++tm) {
+            alo[tm] = alo_n[tm];
+            ahi[tm] = ahi_n[tm];
+        }
+#pragma unroll
+        for (int tn = 0; tn < WN; ++tn) {
+            bw[tn] = bw_n[tn];
+            bs[tn] = bs_n[tn];
+        }
+    }
+
+    if (lb != nullptr && blockIdx.y == 0) {
+        // LoRA epilogue: + lscale * T[m0.., :R] * lb[:R, n0..] on the MFMA, r in the K slot.
+#pragma unroll
+        for (int tm = 0; tm < WM; ++tm) {
+            const int row = min(m0 + 16 * tm + j, M - 1);
+#pragma unroll
+            for (int tn = 0; tn < WN; ++tn) {
+                const int col = min(n0 + 16 * tn + j, N - 1);
+                f32x4 P = zero;
+                for (int r0 = 0; r0 < R; r0 += 4) {
+                    const int r = r0 + q;
+                    const float av = r < R ? lt[static_cast<size_t>(row) * R + r] : 0.0f;
+                    const float bv = r < R ? lb[static_cast<size_t>(r) * N + col] : 0.0f;
+                    P = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, P, 0, 0, 0);
+                }
+                const double s = static_cast<double>(lscale);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[tm][tn][i] = fma(s, static_cast<double>(P[i]), acc[tm][tn][i]);
+            }
+        }
+    }
+
+    float* dst = out + static_cast<size_t>(blockIdx.y) * M * N;
+#pragma unroll
+    for (int tm = 0; tm < WM; ++tm) {
+#pragma unroll
+        for (int tn = 0; tn < WN; ++tn) {
+            const int col = n0 + 16 * tn + j;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = m0 + 16 * tm + 4 * q + i;
+                if (row < M && col < N) dst[static_cast<size_t>(row) * N + col] = static_cast<float>(acc[tm][tn][i]);
+            }
+        }
+    }
+}
+
+// T[m][r] = sum_k x[m][k] * la[k][r], accumulated in double. Grid (M, ceil(R/16)).
+__global__ __launch_bounds__(256) void lora_t_kernel(const float* __restrict__ x,
+                                                     const float* __restrict__ la,
+                                                     float* __restrict__ t, int K, int R) {
+    __shared__ double part[4][16];
+    const int row = blockIdx.x;
+    const int r0 = blockIdx.y * 16;
+    double acc[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.0;
+    const float* xr = x + static_cast<size_t>(row) * K;
+    for (int k = threadIdx.x; k < K; k += blockDim.x) {
+        const double xv = static_cast<double>(xr[k]);
+        const float* lr = la + static_cast<size_t>(k) * R + r0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if (r0 + i < R) acc[i] = fma(xv, static_cast<double>(lr[i]), acc[i]);
+    }
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const double v = wave_sum(acc[i]);
+        if (lane == 0) part[wid][i] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < 16 && r0 + static_cast<int>(threadIdx.x) < R) {
+        const int i = threadIdx.x;
+        t[static_cast<size_t>(row) * R + r0 + i] =
+            static_cast<float>((part[0][i] + part[1][i]) + (part[2][i] + part[3][i]));
+    }
+}
+
+// y[i] = sum_s part[s][i], in ascending s, accumulated in double.
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ part,
+                                                           float* __restrict__ y, size_t count,
+                                                           int splits) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += stride) {
+        double s = 0.0;
+        for (int z = 0; z < splits; ++z) s += static_cast<double>(part[static_cast<size_t>(z) * count + i]);
+        y[i] = static_cast<float>(s);
+    }
+}
+
+template <int WM, int WN, int WAVES_M, int WAVES_N>
+hipError_t launch_mfma(const float* x, const uint8_t* w_packed, const float* w_scales, float* out,
+                       uint32_t m, uint32_t n, uint32_t k, int splits, const float* lt,
+                       const float* lb, uint32_t rank, float lscale, hipStream_t stream) {
+    using Shape = TileShape<WM, WN, WAVES_M, WAVES_N>;
+    const int tiles_m = static_cast<int>((m + Shape::kBM - 1) / Shape::kBM);
+    const int tiles_n = static_cast<int>((n + Shape::kBN - 1) / Shape::kBN);
+    const int G = static_cast<int>(k / kGroup);
+    const int gps = (G + splits - 1) / splits;
+    hipLaunchKernelGGL((q4_gemm_mfma_kernel<WM, WN, WAVES_M, WAVES_N>),
+                       dim3(tiles_m * tiles_n, splits), dim3(Shape::kThreads), 0, stream, x,
+                       reinterpret_cast<const uint32_t*>(w_packed), w_scales, out,
+                       static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), tiles_m,
+                       tiles_n, gps, lt, lb, static_cast<int>(rank), lscale);
+    return hipGetLastError();
+}
+
+// Tile shapes: skinny = one 16-row MFMA tile x 256 columns per workgroup
+// (4 waves of 16 x 64); wide = 128 x 128 per workgroup (2 x 2 waves of 64 x 64).
+using SkinnyShape = TileShape<1, 4, 1, 4>;
+using WideShape = TileShape<4, 4, 2, 2>;
+
+size_t align_up(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+}  // namespace
+
+Q4Plan plan_q4gemm(const DeviceInfo& dev, uint32_t m, uint32_t n, uint32_t k, uint32_t rank) {
+    Q4Plan plan{Q4Plan::kGemv, 1, 0};
+    if (rank == 0 && m <= static_cast<uint32_t>(kGemvMaxRows)) {
+        return plan;
+    }
+    int bm, bn, waves_per_tile;
+    if (m <= 32) {
+        plan.kind = Q4Plan::kMfmaSkinny;
+        bm = SkinnyShape::kBM;
+        bn = SkinnyShape::kBN;
+        waves_per_tile = SkinnyShape::kWaves;
+    } else {
+        plan.kind = Q4Plan::kMfmaWide;
+        bm = WideShape::kBM;
+        bn = WideShape::kBN;
+        waves_per_tile = WideShape::kWaves;
+    }
+    const size_t tiles = static_cast<size_t>((m + bm - 1) / bm) * ((n + bn - 1) / bn);
+    const size_t waves = tiles * waves_per_tile;
+    const size_t target = static_cast<size_t>(8) * dev.cu_count;  // two waves per SIMD
+    const int groups = static_cast<int>(k / kGroup);
+    int splits = 1;
+    while (waves * splits * 2 <= target && groups / (splits * 2) >= 4) splits *= 2;
+    // Re-derive so that no split is empty.
+    const int gps = (groups + splits - 1) / splits;
+    splits = (groups + gps - 1) / gps;
+    plan.splits = splits;
+    size_t bytes = 0;
+    if (splits > 1) bytes += align_up(static_cast<size_t>(splits) * m * n * sizeof(float));
+    if (rank > 0) bytes += align_up(static_cast<size_t>(m) * rank * sizeof(float));
+    plan.workspace_bytes = bytes;
+    return plan;
+}
+
+hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float* x,
+                         const uint8_t* w_packed, const float* w_scales, float* y, uint32_t m,
+                         uint32_t n, uint32_t k, const float* la, const float* lb, uint32_t rank,
+                         float lora_scale, void* workspace, hipStream_t stream) {
+    if (plan.kind == Q4Plan::kGemv) return launch_gemv(dev, x, w_packed, w_scales, y, m, n, k, stream);
+
+    char* wsp = static_cast<char*>(workspace);
+    float* partial = nullptr;
+    if (plan.splits > 1) {
+        partial = reinterpret_cast<float*>(wsp);
+        wsp += align_up(static_cast<size_t>(plan.splits) * m * n * sizeof(float));
+    }
+    float* t = nullptr;
+    if (rank > 0) {
+        t = reinterpret_cast<float*>(wsp);
+        hipLaunchKernelGGL(lora_t_kernel, dim3(m, (rank + 15) / 16), dim3(256), 0, stream, x, la, t,
+                           static_cast<int>(k), static_cast<int>(rank));
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    float* out = plan.splits > 1 ? partial : y;
+    hipError_t e;
+    if (plan.kind == Q4Plan::kMfmaSkinny) {
+        e = launch_mfma<1, 4, 1, 4>(x, w_packed, w_scales, out, m, n, k, plan.splits, t, rank ? lb : nullptr,
+                                    rank, lora_scale, stream);
+    } else {
+        e = launch_mfma<4, 4, 2, 2>(x, w_packed, w_scales, out, m, n, k, plan.splits, t, rank ? lb : nullptr,
+                                    rank, lora_scale, stream);
+    }
+    if (e != hipSuccess || plan.splits == 1) return e;
+    const size_t count = static_cast<size_t>(m) * n;
+    size_t blocks = (count + 255) / 256;
+    const size_t cap = static_cast<size_t>(dev.cu_count) * 8;
+    if (blocks > cap) blocks = cap;
+    hipLaunchKernelGGL(split_reduce_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                       partial, y, count, plan.splits);
+    return hipGetLastError();
+}
+
+}  // namespace spaceslug

@@ -1,0 +1,401 @@
+// Decode GEMV for 1..4 rows: y[m][n] = sum_k x[m][k] * v(k, n) * s(n, k/32).
+//
+// HBM-bound: one pass over the packed weights and scales. Work mapping:
+//   - a wavefront owns CPW consecutive columns; lane l owns the scale groups
+//     g = l, l + 64, ... of each. A column's packed bytes are contiguous
+//     (q4gemm.comp:13, byte n*(K/2) + k/2), so for one column the 64 lanes'
+//     16-byte loads cover 1 KiB of contiguous memory: every weight load is a
+//     fully coalesced 128-bit load, and a lane's 16 bytes are exactly one
+//     32-value scale group. The lane's scale s(n, g) is one coalesced 32-bit
+//     load (lanes hold consecutive groups of the column), so no LDS broadcast
+//     is needed: each scale is read once, by the one lane that applies it;
+//   - all weight and scale loads of the wavefront's columns for a K chunk are
+//     issued before any arithmetic, so the whole wavefront's data is in flight
+//     at once; the columns are then consumed in issue order as they land;
+//   - x stays in registers for the whole chunk (the lane's own groups), read
+//     straight from global memory (it is tiny and L1/L2 resident), together
+//     with each group's pairwise sum of x divided by 64;
+//   - nibbles are decoded in registers to (v + 8) * 2^-9 by v_cvt_pk_f32_fp8
+//     (nibbles_offset_e4m3), so a group partial is
+//     sum x (v + 8) 2^-9 - sum x / 64 = 2^-9 * sum x v; it is scaled by s and
+//     accumulated per lane; the 64 lane partials of a column are summed with
+//     DPP row operations plus two row broadcasts, and the 2^9 factor restored
+//     exactly at the end.
+// K larger than one chunk (64 * SPC groups per lane pass) is walked in chunks.
+#include "q4_device.hpp"
+#include "q4_kernels.hpp"
+
+namespace spaceslug {
+namespace {
+
+constexpr int kGemvThreads = 256;
+
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_src(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+
+// Sum over the 64 lanes; every lane receives the total (readlane of lane 63).
+__device__ __forceinline__ float wave_reduce_dpp(float v) {
+    v += dpp_src<0xB1>(v);         // quad_perm [1,0,3,2]: pairs
+    v += dpp_src<0x4E>(v);         // quad_perm [2,3,0,1]: quads
+    v += dpp_src<0x141>(v);        // row_half_mirror: 8-lane halves
+    v += dpp_src<0x140>(v);        // row_mirror: 16-lane rows
+    v += dpp_src<0x142, 0xA>(v);   // row_bcast:15 into rows 1 and 3
+    v += dpp_src<0x143, 0xC>(v);   // row_bcast:31 into rows 2 and 3 -> row 3 holds the total
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Pairwise sum of 32 floats (error grows with log2(32), not 32).
+__device__ __forceinline__ float pairwise32(const float (&v)[32]) {
+    float t[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t[i] = v[2 * i] + v[2 * i + 1];
+#pragma unroll
+    for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+        for (int i = 0; i < w; ++i) t[i] = t[2 * i] + t[2 * i + 1];
+    return t[0];
+}
+
+// Loads of one K chunk for CPW columns: x first (coalesced, into xr), then every
+// weight and scale word. Kept in one straight-line block so the memory counters,
+// which retire loads in issue order, release x before any weight data.
+template <int M, int SPC, int CPW>
+struct ChunkLoads {
+    static constexpr int kChunkF4 = 64 * SPC * 8;  // float4 of x per row and chunk
+    static constexpr int kPerThread = kChunkF4 / kGemvThreads;
+    static_assert(kChunkF4 % kGemvThreads == 0, "x chunk must split evenly over the workgroup");
+    f32x4 xr[M][kPerThread];
+    u32x4 wv[CPW][SPC];
+    float sc[CPW][SPC];
+};
+
+template <int M, int SPC, int CPW>
+__device__ __forceinline__ void issue_chunk(ChunkLoads<M, SPC, CPW>& L, const float* x,
+                                            const u32x4* __restrict__ wq, const float* __restrict__ ws, int N,
+                                            int K, int G, int col0, int g0, int lane) {
+    using CL = ChunkLoads<M, SPC, CPW>;
+    const int c4_begin = g0 * 8;
+    const int c4_last = min(CL::kChunkF4, (K >> 2) - c4_begin) - 1;
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int i = 0; i < CL::kPerThread; ++i) {
+            // slots past K repeat the last chunk; their groups get a zero scale
+            const int c = min(static_cast<int>(threadIdx.x) + i * kGemvThreads, c4_last);
+            L.xr[m][i] = reinterpret_cast<const f32x4*>(x + static_cast<size_t>(m) * K)[c4_begin + c];
+        }
+    // Compiler-only fence: no load moves across it, so x is issued before the weights
+    // (x is deliberately not __restrict__, which would let its loads sink past it).
+    asm volatile("" ::: "memory");
+    // Column bases are wave-uniform (SGPR); the lane's offset is one unsigned 32-bit
+    // byte offset, so each load is SGPR base + VGPR offset.
+    uint32_t off16[SPC], off4[SPC];
+#pragma unroll
+    for (int s = 0; s < SPC; ++s) {
+        const uint32_t g = static_cast<uint32_t>(min(g0 + 64 * s + lane, G - 1));
+        off16[s] = g * 16u;
+        off4[s] = g * 4u;
+    }
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+        const size_t base = static_cast<size_t>(min(col0 + c, N - 1)) * G;
+        const char* wcol = reinterpret_cast<const char*>(wq + base);
+        const char* scol = reinterpret_cast<const char*>(ws + base);
+#pragma unroll
+        for (int s = 0; s < SPC; ++s) {
+            L.wv[c][s] = *reinterpret_cast<const u32x4*>(wcol + off16[s]);
+            L.sc[c][s] = *reinterpret_cast<const float*>(scol + off4[s]);
+        }
+    }
+    asm volatile("" ::: "memory");
+}
+
+template <int M, int SPC, int CPW>
+__device__ __forceinline__ void consume_chunk(ChunkLoads<M, SPC, CPW>& L, f32x4* xs, float (&acc)[CPW][M], int G,
+                                              int g0, int lane) {
+    using CL = ChunkLoads<M, SPC, CPW>;
+    // x to LDS (chunk q of group g at slot g*8 + (q ^ (g & 7)): a wavefront's 128-bit
+    // reads of 64 groups then hit 8 distinct 16-byte bank groups per 8 lanes).
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int i = 0; i < CL::kPerThread; ++i) {
+            const int c = static_cast<int>(threadIdx.x) + i * kGemvThreads;
+            const int g = c >> 3, q = c & 7;
+            xs[m * CL::kChunkF4 + (g << 3) + (q ^ (g & 7))] = L.xr[m][i];
+        }
+    __syncthreads();
+    float xv[M][SPC][32];
+    float cr[M][SPC];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+#pragma unroll
+        for (int s = 0; s < SPC; ++s) {
+            const int gl = 64 * s + lane;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const f32x4 t = xs[m * CL::kChunkF4 + (gl << 3) + (q ^ (gl & 7))];
+                xv[m][s][4 * q + 0] = t[0];
+                xv[m][s][4 * q + 1] = t[1];
+                xv[m][s][4 * q + 2] = t[2];
+                xv[m][s][4 * q + 3] = t[3];
+            }
+            cr[m][s] = pairwise32(xv[m][s]) * (1.0f / 64.0f);
+        }
+    }
+    // Groups past K contribute through a zero scale: a select, not a branch, so no
+    // branch splits the batch of outstanding loads.
+#pragma unroll
+    for (int c = 0; c < CPW; ++c)
+#pragma unroll
+        for (int s = 0; s < SPC; ++s) L.sc[c][s] = (g0 + 64 * s + lane < G) ? L.sc[c][s] : 0.0f;
+
+    // Columns in issue order, each as soon as its loads have landed.
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+#pragma unroll
+        for (int s = 0; s < SPC; ++s) {
+            float f[32];
+#pragma unroll
+            for (int w = 0; w < 4; ++w) nibbles_offset_e4m3(L.wv[c][s][w], *reinterpret_cast<float(*)[8]>(&f[8 * w]));
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                float p0 = 0.0f, p1 = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 16; ++k) {
+                    p0 = fmaf(xv[m][s][k], f[k], p0);
+                    p1 = fmaf(xv[m][s][16 + k], f[16 + k], p1);
+                }
+                const float d = (p0 + p1) - cr[m][s];
+                acc[c][m] = fmaf(L.sc[c][s], d, acc[c][m]);
+            }
+        }
+    }
+}
+
+// SINGLE: K fits one chunk (G <= 64 * SPC), straight-line code; otherwise K is
+// walked chunk by chunk.
+template <int M, int SPC, int CPW, bool SINGLE>
+__global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const float* x,  // not restrict: see issue_chunk
+                                                              const u32x4* __restrict__ wq,
+                                                              const float* __restrict__ ws,
+                                                              float* __restrict__ y, int N, int K) {
+    using CL = ChunkLoads<M, SPC, CPW>;
+    __shared__ f32x4 xs[M * CL::kChunkF4];
+    const int lane = threadIdx.x & 63;
+    // The wavefront index is uniform; readfirstlane keeps it and every column base
+    // derived from it in SGPRs. Every wavefront takes part in the barriers;
+    // past-the-end wavefronts work on a clamped column and store nothing.
+    const int wave =
+        __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)));
+    const int col0 = wave * CPW;
+    const int G = K >> 5;
+
+    float acc[CPW][M];
+#pragma unroll
+    for (int c = 0; c < CPW; ++c)
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[c][m] = 0.0f;
+
+    if constexpr (SINGLE) {
+        CL L;
+        issue_chunk<M, SPC, CPW>(L, x, wq, ws, N, K, G, col0, 0, lane);
+        consume_chunk<M, SPC, CPW>(L, xs, acc, G, 0, lane);
+    } else {
+        for (int g0 = 0; g0 < G; g0 += 64 * SPC) {
+            CL L;
+            issue_chunk<M, SPC, CPW>(L, x, wq, ws, N, K, G, col0, g0, lane);
+            if (g0 > 0) __syncthreads();  // previous chunk's LDS reads are done
+            consume_chunk<M, SPC, CPW>(L, xs, acc, G, g0, lane);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+        const int col = col0 + c;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const float total = wave_reduce_dpp(acc[c][m]);
+            if (lane == 0 && col < N) y[static_cast<size_t>(m) * N + col] = total * kE4m3OffsetUnit;
+        }
+    }
+}
+
+// Software-pipelined single-row decode (M = 1, K <= 64 * SPC * 32): each wavefront
+// owns CPB = D * ITERS consecutive columns and keeps D columns of loads in flight,
+// computing column i while columns i+1 .. i+D stream in. x is staged once per
+// workgroup in LDS and held in registers for all of the wavefront's columns.
+template <int SPC, int D>
+struct PipeSlot {
+    u32x4 wv[SPC];
+    float sc[SPC];
+};
+
+template <int SPC, int D>
+__device__ __forceinline__ void pipe_issue(PipeSlot<SPC, D>& slot, const u32x4* __restrict__ wq,
+                                           const float* __restrict__ ws, int col, int N, int G,
+                                           const uint32_t (&off16)[SPC], const uint32_t (&off4)[SPC]) {
+    const size_t base = static_cast<size_t>(min(col, N - 1)) * G;
+    const char* wcol = reinterpret_cast<const char*>(wq + base);
+    const char* scol = reinterpret_cast<const char*>(ws + base);
+#pragma unroll
+    for (int s = 0; s < SPC; ++s) {
+        slot.wv[s] = *reinterpret_cast<const u32x4*>(wcol + off16[s]);
+        slot.sc[s] = *reinterpret_cast<const float*>(scol + off4[s]);
+    }
+}
+
+template <int SPC, int D>
+__device__ __forceinline__ float pipe_column(const PipeSlot<SPC, D>& slot, const float (&xv)[SPC][32],
+                                             const float (&cr)[SPC], const bool (&valid)[SPC]) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int s = 0; s < SPC; ++s) {
+        float f[32];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) nibbles_offset_e4m3(slot.wv[s][w], *reinterpret_cast<float(*)[8]>(&f[8 * w]));
+        float p0 = 0.0f, p1 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            p0 = fmaf(xv[s][k], f[k], p0);
+            p1 = fmaf(xv[s][16 + k], f[16 + k], p1);
+        }
+        const float sc = valid[s] ? slot.sc[s] : 0.0f;
+        acc = fmaf(sc, (p0 + p1) - cr[s], acc);
+    }
+    return wave_reduce_dpp(acc);
+}
+
+template <int SPC, int D, bool STRIDED>
+__global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float* x,  // not restrict: see issue_chunk
+                                                                   const u32x4* __restrict__ wq,
+                                                                   const float* __restrict__ ws,
+                                                                   float* __restrict__ y, int N, int K, int iters) {
+    constexpr int kChunkF4 = 64 * SPC * 8;
+    constexpr int kPerThread = kChunkF4 / kGemvThreads;
+    static_assert(kChunkF4 % kGemvThreads == 0, "x chunk must split evenly over the workgroup");
+    __shared__ f32x4 xs[kChunkF4];
+    const int lane = threadIdx.x & 63;
+    const int wave =
+        __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)));
+    const int cpb = D * iters;  // columns per wavefront (<= 64)
+    const int nwaves = static_cast<int>(gridDim.x * (blockDim.x >> 6));
+    // Column of the wavefront's i-th step: contiguous runs per wavefront, or
+    // grid-strided so that at step i all wavefronts together read one band.
+    auto column = [&](int i) { return STRIDED ? i * nwaves + wave : wave * cpb + i; };
+    const int col0 = wave * cpb;
+    const int G = K >> 5;
+
+    // x first (coalesced), then the first D columns, all before any wait.
+    const int c4_last = (K >> 2) - 1;
+    f32x4 xr[kPerThread];
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i)
+        xr[i] = reinterpret_cast<const f32x4*>(x)[min(static_cast<int>(threadIdx.x) + i * kGemvThreads, c4_last)];
+    asm volatile("" ::: "memory");
+    uint32_t off16[SPC], off4[SPC];
+    bool valid[SPC];
+#pragma unroll
+    for (int s = 0; s < SPC; ++s) {
+        const int g = 64 * s + lane;
+        valid[s] = g < G;
+        const uint32_t gc = static_cast<uint32_t>(min(g, G - 1));
+        off16[s] = gc * 16u;
+        off4[s] = gc * 4u;
+    }
+    PipeSlot<SPC, D> slot[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        pipe_issue<SPC, D>(slot[d], wq, ws, column(d), N, G, off16, off4);
+        // slot by slot, as in the steady state, so the loop's load counts line up
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    asm volatile("" ::: "memory");
+
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i) {
+        const int c = static_cast<int>(threadIdx.x) + i * kGemvThreads;
+        const int g = c >> 3, q = c & 7;
+        xs[(g << 3) + (q ^ (g & 7))] = xr[i];
+    }
+    __syncthreads();
+    float xv[SPC][32];
+    float cr[SPC];
+#pragma unroll
+    for (int s = 0; s < SPC; ++s) {
+        const int gl = 64 * s + lane;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const f32x4 t = xs[(gl << 3) + (q ^ (gl & 7))];
+            xv[s][4 * q + 0] = t[0];
+            xv[s][4 * q + 1] = t[1];
+            xv[s][4 * q + 2] = t[2];
+            xv[s][4 * q + 3] = t[3];
+        }
+        cr[s] = pairwise32(xv[s]) * (1.0f / 64.0f);
+    }
+
+    // Steady state: compute slot d (column i), then refill it with column i + D.
+    float result = 0.0f;
+    int i = 0;
+    for (int it = 0; it + 1 < iters; ++it) {
+#pragma unroll
+        for (int d = 0; d < D; ++d, ++i) {
+            const float t = pipe_column<SPC, D>(slot[d], xv, cr, valid);
+            if (STRIDED) {
+                if (lane == 0 && column(i) < N) y[column(i)] = t * kE4m3OffsetUnit;
+            } else {
+                result = lane == i ? t : result;
+            }
+            pipe_issue<SPC, D>(slot[d], wq, ws, column(i + D), N, G, off16, off4);
+            // Keep the next slot's arithmetic below this refill: otherwise the scheduler
+            // interleaves slots and must wait for every outstanding load first.
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d, ++i) {
+        const float t = pipe_column<SPC, D>(slot[d], xv, cr, valid);
+        if (STRIDED) {
+            if (lane == 0 && column(i) < N) y[column(i)] = t * kE4m3OffsetUnit;
+        } else {
+            result = lane == i ? t : result;
+        }
+    }
+    if (!STRIDED && lane < cpb && col0 + lane < N) y[col0 + lane] = result * kE4m3OffsetUnit;
+}
+
+template <int M, int SPC, int CPW>
+hipError_t launch_rows(const float* x, const uint8_t* w_packed, const float* w_scales, float* y, uint32_t n,
+                       uint32_t k, hipStream_t stream) {
+    const size_t waves = (static_cast<size_t>(n) + CPW - 1) / CPW;
+    const size_t blocks = (waves + kGemvThreads / 64 - 1) / (kGemvThreads / 64);
+    const bool single = (k / kGroup) <= static_cast<uint32_t>(64 * SPC);
+    if (single) {
+        hipLaunchKernelGGL((q4_gemv_kernel<M, SPC, CPW, true>), dim3(static_cast<unsigned>(blocks)),
+                           dim3(kGemvThreads), 0, stream, x, reinterpret_cast<const u32x4*>(w_packed), w_scales, y,
+                           static_cast<int>(n), static_cast<int>(k));
+    } else {
+        hipLaunchKernelGGL((q4_gemv_kernel<M, SPC, CPW, false>), dim3(static_cast<unsigned>(blocks)),
+                           dim3(kGemvThreads), 0, stream, x, reinterpret_cast<const u32x4*>(w_packed), w_scales, y,
+                           static_cast<int>(n), static_cast<int>(k));
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gemv(const DeviceInfo& dev, const float* x, const uint8_t* w_packed, const float* w_scales,
+                       float* y, uint32_t m, uint32_t n, uint32_t k, hipStream_t stream) {
+    (void)dev;
+    switch (m) {
+        case 1: return launch_rows<1, 2, 8>(x, w_packed, w_scales, y, n, k, stream);
+        case 2: return launch_rows<2, 2, 4>(x, w_packed, w_scales, y, n, k, stream);
+        case 3: return launch_rows<3, 1, 4>(x, w_packed, w_scales, y, n, k, stream);
+        case 4: return launch_rows<4, 1, 4>(x, w_packed, w_scales, y, n, k, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace spaceslug

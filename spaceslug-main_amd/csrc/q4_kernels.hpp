@@ -1,0 +1,50 @@
+// Internal launch interface between the C-ABI layer (runtime_abi.cpp) and the
+// gfx950 kernels (q4_gemv.hip, q4_gemm.hip, sgemm.hip). Device pointers only;
+// every function enqueues on `stream` and returns hipSuccess or the launch error.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace spaceslug {
+
+// Scale group along K (q4gemm.comp:41,121): one fp32 scale per 32 K values.
+constexpr int kGroup = 32;
+
+// The decode GEMV handles 1..kGemvMaxRows rows; taller inputs go to the MFMA kernel.
+constexpr int kGemvMaxRows = 4;
+
+// Launch shape chosen by plan_q4gemm for one call.
+struct Q4Plan {
+    enum Kind { kGemv, kMfmaSkinny, kMfmaWide } kind;
+    int splits;            // K-splits of the MFMA kernel (1 = write y directly)
+    size_t workspace_bytes;  // device scratch the call needs (split partials + LoRA T)
+};
+
+struct DeviceInfo {
+    int cu_count;
+    size_t max_lds_bytes;
+};
+
+// Decides the kernel and K-split for (m, n, k, rank). rank == 0 means no LoRA.
+Q4Plan plan_q4gemm(const DeviceInfo& dev, uint32_t m, uint32_t n, uint32_t k, uint32_t rank);
+
+// Decode GEMV, 1 <= m <= kGemvMaxRows (no LDS, no device memory beyond its arguments).
+hipError_t launch_gemv(const DeviceInfo& dev, const float* x, const uint8_t* w_packed,
+                       const float* w_scales, float* y, uint32_t m, uint32_t n, uint32_t k,
+                       hipStream_t stream);
+
+// y = x * dequant(W) [+ scale * (x * la) * lb]. `workspace` must hold
+// plan.workspace_bytes bytes (may be null when that is 0).
+hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float* x,
+                         const uint8_t* w_packed, const float* w_scales, float* y, uint32_t m,
+                         uint32_t n, uint32_t k, const float* la, const float* lb, uint32_t rank,
+                         float lora_scale, void* workspace, hipStream_t stream);
+
+// fp32 C = A * B, row-major, m % 64 == 0, n % 64 == 0, k % 32 == 0 (checked by the caller).
+hipError_t launch_sgemm(const float* a, const float* b, float* c, uint32_t m, uint32_t n,
+                        uint32_t k, hipStream_t stream);
+
+}  // namespace spaceslug

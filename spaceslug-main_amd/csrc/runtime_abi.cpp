@@ -1,0 +1,383 @@
+// C-ABI layer of libspaceslug_runtime.so (declarations and contracts in
+// include/runtime_abi.h). Host C++ calling HIP directly: argument validation
+// first (so contract violations return 1 without touching a device), then
+// per-device state, staging of host buffers, the kernel launch and, for the
+// synchronous entry points, the copy back. Every HIP failure and every C++
+// exception is turned into status 2 with a message in spaceslug_last_error();
+// the int4 path has no CPU implementation, so without a HIP device every
+// compute entry point returns 2.
+#include "runtime_abi.h"
+
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cstdint>
+#include <cstring>
+#include <exception>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "q4_kernels.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& message) {
+    g_last_error = message;
+    return code;
+}
+
+int ok() {
+    g_last_error.clear();
+    return SPACESLUG_OK;
+}
+
+struct HipError {
+    hipError_t code;
+    const char* what;
+};
+
+void check(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw HipError{e, what};
+}
+
+int from_hip(const HipError& e) {
+    return fail(SPACESLUG_ERR_DEVICE, std::string(e.what) + ": " + hipGetErrorName(e.code) + " (" +
+                                          hipGetErrorString(e.code) + ")");
+}
+
+// Per-device state: launch-relevant properties and the grow-only workspace of
+// the device-pointer entry points.
+struct DeviceState {
+    bool ready = false;
+    spaceslug::DeviceInfo info{};
+    void* workspace = nullptr;
+    size_t workspace_bytes = 0;
+};
+
+std::mutex g_device_mutex;
+std::vector<DeviceState> g_devices;
+
+// Number of visible devices, queried once (the set of devices is fixed for the process).
+int device_count() {
+    static int cached = -1;
+    if (cached < 0) {
+        int count = 0;
+        hipError_t e = hipGetDeviceCount(&count);
+        if (e != hipSuccess || count <= 0) throw HipError{e == hipSuccess ? hipErrorNoDevice : e, "no HIP device"};
+        cached = count;
+    }
+    return cached;
+}
+
+DeviceState& current_device() {
+    const int count = device_count();
+    int id = 0;
+    check(hipGetDevice(&id), "hipGetDevice");
+    std::lock_guard<std::mutex> lock(g_device_mutex);
+    if (g_devices.size() < static_cast<size_t>(count)) g_devices.resize(count);
+    DeviceState& d = g_devices[id];
+    if (!d.ready) {
+        hipDeviceProp_t prop;
+        check(hipGetDeviceProperties(&prop, id), "hipGetDeviceProperties");
+        d.info.cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 1;
+        d.info.max_lds_bytes = prop.sharedMemPerBlock;
+        d.ready = true;
+    }
+    return d;
+}
+
+// Returns the device workspace holding at least `bytes`; growing it waits for
+// the device so no queued kernel still reads the old buffer.
+void* device_workspace(DeviceState& d, size_t bytes) {
+    if (bytes == 0) return nullptr;
+    std::lock_guard<std::mutex> lock(g_device_mutex);
+    if (d.workspace_bytes < bytes) {
+        if (d.workspace) {
+            check(hipDeviceSynchronize(), "hipDeviceSynchronize (workspace growth)");
+            check(hipFree(d.workspace), "hipFree (workspace)");
+            d.workspace = nullptr;
+            d.workspace_bytes = 0;
+        }
+        check(hipMalloc(&d.workspace, bytes), "hipMalloc (workspace)");
+        d.workspace_bytes = bytes;
+    }
+    return d.workspace;
+}
+
+// One device allocation carved into 256-byte aligned slices; freed on scope exit.
+class StagingArena {
+public:
+    explicit StagingArena(const std::vector<size_t>& sizes) {
+        size_t total = 0;
+        for (size_t s : sizes) {
+            offsets_.push_back(total);
+            total += (s + 255) & ~static_cast<size_t>(255);
+        }
+        if (total == 0) total = 256;
+        check(hipMalloc(&base_, total), "hipMalloc (staging)");
+    }
+    ~StagingArena() {
+        if (base_) (void)hipFree(base_);
+    }
+    StagingArena(const StagingArena&) = delete;
+    StagingArena& operator=(const StagingArena&) = delete;
+    template <typename T>
+    T* slice(size_t i) const {
+        return reinterpret_cast<T*>(static_cast<char*>(base_) + offsets_[i]);
+    }
+
+private:
+    void* base_ = nullptr;
+    std::vector<size_t> offsets_;
+};
+
+bool dims_ok(uint32_t m, uint32_t n, uint32_t k) {
+    return m >= 1 && n >= 1 && k >= 32 && (k % spaceslug::kGroup) == 0 && m <= INT32_MAX &&
+           n <= INT32_MAX && k <= INT32_MAX;
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+size_t bytes_x(uint32_t m, uint32_t k) { return static_cast<size_t>(m) * k * sizeof(float); }
+size_t bytes_w(uint32_t n, uint32_t k) { return static_cast<size_t>(n) * (k / 2); }
+size_t bytes_s(uint32_t n, uint32_t k) { return static_cast<size_t>(n) * (k / spaceslug::kGroup) * sizeof(float); }
+size_t bytes_y(uint32_t m, uint32_t n) { return static_cast<size_t>(m) * n * sizeof(float); }
+
+// Shared body of the synchronous host-pointer calls (with or without LoRA, with
+// or without pre-resident weights).
+int run_host(const float* x, const uint8_t* w, const float* s, const uint8_t* d_w_resident,
+             const float* d_s_resident, const float* la, const float* lb, float* y, uint32_t m,
+             uint32_t n, uint32_t k, uint32_t rank, float lora_scale) {
+    DeviceState& dev = current_device();
+    const spaceslug::Q4Plan plan = spaceslug::plan_q4gemm(dev.info, m, n, k, rank);
+    const bool stage_w = d_w_resident == nullptr;
+    std::vector<size_t> sizes = {bytes_x(m, k), bytes_y(m, n), plan.workspace_bytes,
+                                 stage_w ? bytes_w(n, k) : 0, stage_w ? bytes_s(n, k) : 0,
+                                 rank ? static_cast<size_t>(k) * rank * sizeof(float) : 0,
+                                 rank ? static_cast<size_t>(rank) * n * sizeof(float) : 0};
+    StagingArena arena(sizes);
+    float* dx = arena.slice<float>(0);
+    float* dy = arena.slice<float>(1);
+    void* dws = plan.workspace_bytes ? arena.slice<void>(2) : nullptr;
+    const uint8_t* dw = d_w_resident;
+    const float* ds = d_s_resident;
+    if (stage_w) {
+        check(hipMemcpy(arena.slice<uint8_t>(3), w, bytes_w(n, k), hipMemcpyHostToDevice), "hipMemcpy (weights)");
+        check(hipMemcpy(arena.slice<float>(4), s, bytes_s(n, k), hipMemcpyHostToDevice), "hipMemcpy (scales)");
+        dw = arena.slice<uint8_t>(3);
+        ds = arena.slice<float>(4);
+    }
+    float* dla = nullptr;
+    float* dlb = nullptr;
+    if (rank) {
+        dla = arena.slice<float>(5);
+        dlb = arena.slice<float>(6);
+        check(hipMemcpy(dla, la, static_cast<size_t>(k) * rank * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy (lora_a)");
+        check(hipMemcpy(dlb, lb, static_cast<size_t>(rank) * n * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy (lora_b)");
+    }
+    check(hipMemcpy(dx, x, bytes_x(m, k), hipMemcpyHostToDevice), "hipMemcpy (x)");
+    check(spaceslug::launch_q4gemm(plan, dev.info, dx, dw, ds, dy, m, n, k, dla, dlb, rank, lora_scale, dws, nullptr),
+          "q4gemm launch");
+    check(hipMemcpy(y, dy, bytes_y(m, n), hipMemcpyDeviceToHost), "hipMemcpy (y)");
+    return ok();
+}
+
+int run_device(const float* dx, const uint8_t* dw, const float* ds, const float* dla, const float* dlb,
+               float* dy, uint32_t m, uint32_t n, uint32_t k, uint32_t rank, float lora_scale,
+               void* stream) {
+    DeviceState& dev = current_device();
+    const spaceslug::Q4Plan plan = spaceslug::plan_q4gemm(dev.info, m, n, k, rank);
+    void* dws = device_workspace(dev, plan.workspace_bytes);
+    check(spaceslug::launch_q4gemm(plan, dev.info, dx, dw, ds, dy, m, n, k, dla, dlb, rank, lora_scale, dws,
+                                   static_cast<hipStream_t>(stream)),
+          "q4gemm launch");
+    return ok();
+}
+
+}  // namespace
+
+struct spaceslug_q4_weight {
+    int device;
+    uint32_t n;
+    uint32_t k;
+    uint8_t* d_packed;
+    float* d_scales;
+};
+
+extern "C" {
+
+int spaceslug_vector_add(const float* left, const float* right, float* output, size_t count) {
+    if (!left || !right || !output) return fail(SPACESLUG_ERR_INVALID, "spaceslug_vector_add: null pointer");
+    for (size_t i = 0; i < count; ++i) output[i] = left[i] + right[i];
+    return ok();
+}
+
+int spaceslug_sgemm(const float* a, const float* b, float* c, uint32_t m, uint32_t n, uint32_t k,
+                    float* max_relative_error) {
+    if (!a || !b || !c || !max_relative_error || m == 0 || n == 0 || k == 0 || m % 64 || n % 64 || k % 32 ||
+        m > INT32_MAX || n > INT32_MAX || k > INT32_MAX)
+        return fail(SPACESLUG_ERR_INVALID, "spaceslug_sgemm: invalid arguments (need m%64, n%64, k%32, non-null)");
+    try {
+        (void)current_device();
+        const size_t ab = static_cast<size_t>(m) * k * sizeof(float);
+        const size_t bb = static_cast<size_t>(k) * n * sizeof(float);
+        const size_t cb = static_cast<size_t>(m) * n * sizeof(float);
+        StagingArena arena({ab, bb, cb});
+        check(hipMemcpy(arena.slice<float>(0), a, ab, hipMemcpyHostToDevice), "hipMemcpy (a)");
+        check(hipMemcpy(arena.slice<float>(1), b, bb, hipMemcpyHostToDevice), "hipMemcpy (b)");
+        check(spaceslug::launch_sgemm(arena.slice<float>(0), arena.slice<float>(1), arena.slice<float>(2), m, n, k,
+                                      nullptr),
+              "sgemm launch");
+        check(hipMemcpy(c, arena.slice<float>(2), cb, hipMemcpyDeviceToHost), "hipMemcpy (c)");
+        *max_relative_error = 0.0f;
+        return ok();
+    } catch (const HipError& e) {
+        return from_hip(e);
+    } catch (const std::exception& e) {
+        return fail(SPACESLUG_ERR_DEVICE, e.what());
+    } catch (...) {
+        return fail(SPACESLUG_ERR_DEVICE, "spaceslug_sgemm: unknown exception");
+    }
+}
+
+const char* spaceslug_q4gemm_capability(void) {
+    return "q4gemm-hip-gfx950 group=32 layout=n-major-lsb-nibble decode=gemv(m<=4) prefill=mfma-f32-16x16x4 "
+           "accumulate=f32-group+f64 lora=fused-epilogue(rank<=64)";
+}
+
+const char* spaceslug_last_error(void) { return g_last_error.c_str(); }
+
+int spaceslug_q4gemm(const float* x, const uint8_t* w_packed, const float* w_scales, float* y, uint32_t m,
+                     uint32_t n, uint32_t k) {
+    if (!x || !w_packed || !w_scales || !y) return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm: null pointer");
+    if (!dims_ok(m, n, k)) return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm: need m>=1, n>=1, k>=32, k%32==0");
+    try {
+        return run_host(x, w_packed, w_scales, nullptr, nullptr, nullptr, nullptr, y, m, n, k, 0, 0.0f);
+    } catch (const HipError& e) {
+        return from_hip(e);
+    } catch (const std::exception& e) {
+        return fail(SPACESLUG_ERR_DEVICE, e.what());
+    } catch (...) {
+        return fail(SPACESLUG_ERR_DEVICE, "spaceslug_q4gemm: unknown exception");
+    }
+}
+
+int spaceslug_q4gemm_lora(const float* x, const uint8_t* w_packed, const float* w_scales, const float* lora_a,
+                          const float* lora_b, float* y, uint32_t m, uint32_t n, uint32_t k, uint32_t rank,
+                          float scale) {
+    if (!x || !w_packed || !w_scales || !lora_a || !lora_b || !y)
+        return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_lora: null pointer");
+    if (!dims_ok(m, n, k) || rank == 0 || rank > SPACESLUG_Q4_MAX_LORA_RANK)
+        return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_lora: need m>=1, n>=1, k%32==0, 1<=rank<=64");
+    try {
+        return run_host(x, w_packed, w_scales, nullptr, nullptr, lora_a, lora_b, y, m, n, k, rank, scale);
+    } catch (const HipError& e) {
+        return from_hip(e);
+    } catch (const std::exception& e) {
+        return fail(SPACESLUG_ERR_DEVICE, e.what());
+    } catch (...) {
+        return fail(SPACESLUG_ERR_DEVICE, "spaceslug_q4gemm_lora: unknown exception");
+    }
+}
+
+int spaceslug_q4gemm_device(const float* d_x, const uint8_t* d_w_packed, const float* d_w_scales, float* d_y,
+                            uint32_t m, uint32_t n, uint32_t k, void* stream) {
+    if (!d_x || !d_w_packed || !d_w_scales || !d_y)
+        return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_device: null pointer");
+    if (!dims_ok(m, n, k)) return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_device: need m>=1, n>=1, k%32==0");
+    if (!aligned(d_x, 16) || !aligned(d_w_packed, 16) || !aligned(d_w_scales, 4) || !aligned(d_y, 4))
+        return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_device: misaligned device pointer");
+    try {
+        return run_device(d_x, d_w_packed, d_w_scales, nullptr, nullptr, d_y, m, n, k, 0, 0.0f, stream);
+    } catch (const HipError& e) {
+        return from_hip(e);
+    } catch (const std::exception& e) {
+        return fail(SPACESLUG_ERR_DEVICE, e.what());
+    } catch (...) {
+        return fail(SPACESLUG_ERR_DEVICE, "spaceslug_q4gemm_device: unknown exception");
+    }
+}
+
+int spaceslug_q4gemm_lora_device(const float* d_x, const uint8_t* d_w_packed, const float* d_w_scales,
+                                 const float* d_lora_a, const float* d_lora_b, float* d_y, uint32_t m, uint32_t n,
+                                 uint32_t k, uint32_t rank, float scale, void* stream) {
+    if (!d_x || !d_w_packed || !d_w_scales || !d_lora_a || !d_lora_b || !d_y)
+        return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_lora_device: null pointer");
+    if (!dims_ok(m, n, k) || rank == 0 || rank > SPACESLUG_Q4_MAX_LORA_RANK)
+        return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_lora_device: need m>=1, n>=1, k%32==0, 1<=rank<=64");
+    if (!aligned(d_x, 16) || !aligned(d_w_packed, 16) || !aligned(d_w_scales, 4) || !aligned(d_y, 4) ||
+        !aligned(d_lora_a, 4) || !aligned(d_lora_b, 4))
+        return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_lora_device: misaligned device pointer");
+    try {
+        return run_device(d_x, d_w_packed, d_w_scales, d_lora_a, d_lora_b, d_y, m, n, k, rank, scale, stream);
+    } catch (const HipError& e) {
+        return from_hip(e);
+    } catch (const std::exception& e) {
+        return fail(SPACESLUG_ERR_DEVICE, e.what());
+    } catch (...) {
+        return fail(SPACESLUG_ERR_DEVICE, "spaceslug_q4gemm_lora_device: unknown exception");
+    }
+}
+
+spaceslug_q4_weight* spaceslug_q4_weight_create(const uint8_t* w_packed, const float* w_scales, uint32_t n,
+                                                uint32_t k) {
+    if (!w_packed || !w_scales || !dims_ok(1, n, k)) {
+        fail(SPACESLUG_ERR_INVALID, "spaceslug_q4_weight_create: invalid arguments");
+        return nullptr;
+    }
+    spaceslug_q4_weight* h = nullptr;
+    try {
+        (void)current_device();
+        h = new spaceslug_q4_weight{0, n, k, nullptr, nullptr};
+        check(hipGetDevice(&h->device), "hipGetDevice");
+        check(hipMalloc(reinterpret_cast<void**>(&h->d_packed), bytes_w(n, k)), "hipMalloc (weights)");
+        check(hipMalloc(reinterpret_cast<void**>(&h->d_scales), bytes_s(n, k)), "hipMalloc (scales)");
+        check(hipMemcpy(h->d_packed, w_packed, bytes_w(n, k), hipMemcpyHostToDevice), "hipMemcpy (weights)");
+        check(hipMemcpy(h->d_scales, w_scales, bytes_s(n, k), hipMemcpyHostToDevice), "hipMemcpy (scales)");
+        ok();
+        return h;
+    } catch (const HipError& e) {
+        from_hip(e);
+    } catch (const std::exception& e) {
+        fail(SPACESLUG_ERR_DEVICE, e.what());
+    } catch (...) {
+        fail(SPACESLUG_ERR_DEVICE, "spaceslug_q4_weight_create: unknown exception");
+    }
+    spaceslug_q4_weight_destroy(h);
+    return nullptr;
+}
+
+void spaceslug_q4_weight_destroy(spaceslug_q4_weight* weight) {
+    if (!weight) return;
+    int prev = -1;
+    if (hipGetDevice(&prev) == hipSuccess && prev != weight->device) (void)hipSetDevice(weight->device);
+    if (weight->d_packed) (void)hipFree(weight->d_packed);
+    if (weight->d_scales) (void)hipFree(weight->d_scales);
+    if (prev >= 0 && prev != weight->device) (void)hipSetDevice(prev);
+    delete weight;
+}
+
+int spaceslug_q4gemm_run(const spaceslug_q4_weight* weight, const float* x, float* y, uint32_t m) {
+    if (!weight || !x || !y) return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_run: null pointer");
+    if (!dims_ok(m, weight->n, weight->k)) return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_run: need m>=1");
+    try {
+        int cur = -1;
+        check(hipGetDevice(&cur), "hipGetDevice");
+        if (cur != weight->device)
+            return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_run: weight lives on another device");
+        return run_host(x, nullptr, nullptr, weight->d_packed, weight->d_scales, nullptr, nullptr, y, m, weight->n,
+                        weight->k, 0, 0.0f);
+    } catch (const HipError& e) {
+        return from_hip(e);
+    } catch (const std::exception& e) {
+        return fail(SPACESLUG_ERR_DEVICE, e.what());
+    } catch (...) {
+        return fail(SPACESLUG_ERR_DEVICE, "spaceslug_q4gemm_run: unknown exception");
+    }
+}
+
+}  // extern "C"

@@ -1,0 +1,323 @@
+"""ctypes binding of libspaceslug_runtime.so, mirroring the reference host's conventions.
+
+Reference: python/spaceslug/backend.py
+  - ExecutionResult / BackendError            :28-41
+  - BackendSession._native()                  :56-67  (CDLL, mandatory symbols
+    spaceslug_vector_add and spaceslug_sgemm bound unconditionally, every other
+    symbol probed with hasattr)
+  - execute_sgemm_native                      :571-583
+  - _native_sgemm_values (projection caller)  :1692-1705
+  - execute_tiny_lora_forward's projected()   :794-799 (base + LoRA delta)
+A nonzero status from the library raises BackendError carrying the status and
+spaceslug_last_error(). The int4 path exists only on the GPU: there is no CPU
+fallback, so a missing library or a missing HIP device is an error.
+
+Parity is reported, as in execute_projected_qkv (:585-600), against a
+``cpu_reference`` supplied by the caller; without one the metrics say
+"parity": "not-run".
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import time
+from dataclasses import dataclass, field
+from pathlib import Path
+from typing import Any, Sequence
+
+import numpy as np
+
+from .parity import compare_float_arrays
+
+PACKAGE_ROOT = Path(__file__).resolve().parent.parent
+DEFAULT_LIBRARY = PACKAGE_ROOT / "_lib" / "libspaceslug_runtime.so"
+
+# Status codes of include/runtime_abi.h.
+OK = 0
+ERR_INVALID = 1
+ERR_DEVICE = 2
+ERR_UNSUPPORTED = -4
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_u32 = ctypes.c_uint32
+
+
+def library_path() -> Path:
+    """SPACESLUG_RUNTIME_LIB overrides the in-tree build location."""
+    env = os.environ.get("SPACESLUG_RUNTIME_LIB")
+    return Path(env) if env else DEFAULT_LIBRARY
+
+
+@dataclass(frozen=True)
+class ExecutionResult:
+    status: str
+    operation: str
+    backend: str
+    runtime_revision: str
+    device: str | None
+    fallback_used: bool
+    metrics: dict[str, Any] = field(default_factory=dict)
+    output: dict[str, Any] = field(default_factory=dict)
+
+
+class BackendError(RuntimeError):
+    """A structured backend invocation failure."""
+
+
+def _f32(values: Any, count: int, name: str) -> np.ndarray:
+    arr = np.ascontiguousarray(np.asarray(values, dtype=np.float32).ravel())
+    if arr.size != count:
+        raise BackendError(f"{name} has {arr.size} elements, expected {count}")
+    return arr
+
+
+def _u8(values: Any, count: int, name: str) -> np.ndarray:
+    arr = np.ascontiguousarray(np.asarray(values, dtype=np.uint8).ravel())
+    if arr.size != count:
+        raise BackendError(f"{name} has {arr.size} bytes, expected {count}")
+    return arr
+
+
+class Q4Weight:
+    """Device-resident int4 weights (spaceslug_q4_weight_create / _destroy)."""
+
+    def __init__(self, session: "BackendSession", handle: int, n: int, k: int) -> None:
+        self._session = session
+        self._handle = handle
+        self.n = n
+        self.k = k
+
+    @property
+    def handle(self) -> int:
+        if not self._handle:
+            raise BackendError("Q4Weight is closed")
+        return self._handle
+
+    def run(self, x: Any, m: int) -> np.ndarray:
+        """y[m][n] = x[m][k] * dequant(W), synchronous (spaceslug_q4gemm_run)."""
+        xx = _f32(x, m * self.k, "x")
+        yy = np.empty(m * self.n, dtype=np.float32)
+        lib = self._session._native()
+        code = lib.spaceslug_q4gemm_run(ctypes.c_void_p(self.handle), xx.ctypes.data_as(_f32p),
+                                        yy.ctypes.data_as(_f32p), m)
+        self._session._check(code, "spaceslug_q4gemm_run")
+        return yy.reshape(m, self.n)
+
+    def close(self) -> None:
+        if self._handle:
+            self._session._native().spaceslug_q4_weight_destroy(ctypes.c_void_p(self._handle))
+            self._handle = 0
+
+    def __enter__(self) -> "Q4Weight":
+        return self
+
+    def __exit__(self, *exc: Any) -> None:
+        self.close()
+
+    def __del__(self) -> None:  # best effort; explicit close() is preferred
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class BackendSession:
+    """Runtime session bound to libspaceslug_runtime.so (HIP, gfx950)."""
+
+    def __init__(self, runtime_revision: str = "spaceslug-main_amd", library: str | Path | None = None) -> None:
+        self.runtime_revision = runtime_revision
+        self._library_path = Path(library) if library else library_path()
+        self._library: ctypes.CDLL | None = None
+
+    # -- loading -----------------------------------------------------------------------------
+    def _native(self) -> ctypes.CDLL:
+        if self._library is None:
+            if not self._library_path.is_file():
+                raise BackendError(f"runtime shared library is missing: {self._library_path}")
+            try:
+                lib = ctypes.CDLL(str(self._library_path))
+                vector_add = lib.spaceslug_vector_add
+                vector_add.argtypes = [_f32p, _f32p, _f32p, ctypes.c_size_t]
+                vector_add.restype = ctypes.c_int
+                sgemm = lib.spaceslug_sgemm
+                sgemm.argtypes = [_f32p, _f32p, _f32p, _u32, _u32, _u32, _f32p]
+                sgemm.restype = ctypes.c_int
+            except (OSError, AttributeError) as exc:
+                raise BackendError(f"failed to bind runtime library {self._library_path}: {exc}") from exc
+            if hasattr(lib, "spaceslug_last_error"):
+                lib.spaceslug_last_error.argtypes = []
+                lib.spaceslug_last_error.restype = ctypes.c_char_p
+            if hasattr(lib, "spaceslug_q4gemm_capability"):
+                lib.spaceslug_q4gemm_capability.argtypes = []
+                lib.spaceslug_q4gemm_capability.restype = ctypes.c_char_p
+            if hasattr(lib, "spaceslug_q4gemm"):
+                lib.spaceslug_q4gemm.argtypes = [_f32p, _u8p, _f32p, _f32p, _u32, _u32, _u32]
+                lib.spaceslug_q4gemm.restype = ctypes.c_int
+            if hasattr(lib, "spaceslug_q4gemm_lora"):
+                lib.spaceslug_q4gemm_lora.argtypes = [_f32p, _u8p, _f32p, _f32p, _f32p, _f32p, _u32, _u32, _u32, _u32,
+                                                      ctypes.c_float]
+                lib.spaceslug_q4gemm_lora.restype = ctypes.c_int
+            if hasattr(lib, "spaceslug_q4gemm_device"):
+                lib.spaceslug_q4gemm_device.argtypes = [ctypes.c_void_p] * 4 + [_u32, _u32, _u32, ctypes.c_void_p]
+                lib.spaceslug_q4gemm_device.restype = ctypes.c_int
+            if hasattr(lib, "spaceslug_q4gemm_lora_device"):
+                lib.spaceslug_q4gemm_lora_device.argtypes = ([ctypes.c_void_p] * 6 + [_u32] * 4 +
+                                                             [ctypes.c_float, ctypes.c_void_p])
+                lib.spaceslug_q4gemm_lora_device.restype = ctypes.c_int
+            if hasattr(lib, "spaceslug_q4_weight_create"):
+                lib.spaceslug_q4_weight_create.argtypes = [_u8p, _f32p, _u32, _u32]
+                lib.spaceslug_q4_weight_create.restype = ctypes.c_void_p
+                lib.spaceslug_q4_weight_destroy.argtypes = [ctypes.c_void_p]
+                lib.spaceslug_q4_weight_destroy.restype = None
+                lib.spaceslug_q4gemm_run.argtypes = [ctypes.c_void_p, _f32p, _f32p, _u32]
+                lib.spaceslug_q4gemm_run.restype = ctypes.c_int
+            self._library = lib
+        return self._library
+
+    def _last_error(self) -> str:
+        lib = self._native()
+        if hasattr(lib, "spaceslug_last_error"):
+            msg = lib.spaceslug_last_error()
+            return msg.decode() if msg else ""
+        return ""
+
+    def _check(self, code: int, name: str) -> None:
+        if code != OK:
+            raise BackendError(f"native {name} returned {code}: {self._last_error()}")
+
+    def _require(self, symbol: str) -> ctypes.CDLL:
+        lib = self._native()
+        if not hasattr(lib, symbol):
+            raise BackendError(f"runtime library does not export {symbol}")
+        return lib
+
+    def capability(self) -> str:
+        lib = self._require("spaceslug_q4gemm_capability")
+        return lib.spaceslug_q4gemm_capability().decode()
+
+    # -- reference-compatible entry points -----------------------------------------------------
+    def execute_vector_add(self, left: Sequence[float], right: Sequence[float]) -> ExecutionResult:
+        if len(left) != len(right):
+            raise BackendError("vector_add inputs must have equal length")
+        started = time.perf_counter()
+        lib = self._native()
+        ll, rr = _f32(left, len(left), "left"), _f32(right, len(right), "right")
+        out = np.empty_like(ll)
+        self._check(lib.spaceslug_vector_add(ll.ctypes.data_as(_f32p), rr.ctypes.data_as(_f32p),
+                                             out.ctypes.data_as(_f32p), ll.size), "vector_add")
+        return ExecutionResult("ok", "vector_add", "spaceslug-hip", self.runtime_revision, None, False,
+                               {"operation_count": 1, "host_elapsed_seconds": time.perf_counter() - started},
+                               {"first": float(out[0]) if out.size else None,
+                                "last": float(out[-1]) if out.size else None, "count": int(out.size)})
+
+    def sgemm_values(self, a: Any, b: Any, m: int, n: int, k: int) -> np.ndarray:
+        """fp32 C = A * B through spaceslug_sgemm (m % 64, n % 64, k % 32)."""
+        if m % 64 or n % 64 or k % 32 or m <= 0 or n <= 0 or k <= 0:
+            raise BackendError("native sgemm dimensions or input lengths are invalid")
+        lib = self._native()
+        aa, bb = _f32(a, m * k, "a"), _f32(b, k * n, "b")
+        cc = np.empty(m * n, dtype=np.float32)
+        err = ctypes.c_float()
+        self._check(lib.spaceslug_sgemm(aa.ctypes.data_as(_f32p), bb.ctypes.data_as(_f32p), cc.ctypes.data_as(_f32p),
+                                        m, n, k, ctypes.byref(err)), "sgemm")
+        return cc.reshape(m, n)
+
+    def execute_sgemm_native(self, a: Any, b: Any, m: int, n: int, k: int, *,
+                             cpu_reference: Any | None = None) -> ExecutionResult:
+        values = self.sgemm_values(a, b, m, n, k)
+        metrics = self._parity(values, cpu_reference, 1e-3)
+        return ExecutionResult("ok" if metrics.get("status", "pass") == "pass" else "error", "sgemm", "spaceslug-hip",
+                               self.runtime_revision, None, False, metrics,
+                               {"m": m, "n": n, "k": k, "first": float(values.flat[0]), "values": values})
+
+    # -- int4 projection -------------------------------------------------------------------------
+    def q4gemm_values(self, x: Any, w_packed: Any, w_scales: Any, m: int, n: int, k: int) -> np.ndarray:
+        """y[m][n] = x[m][k] * dequant(W) through spaceslug_q4gemm (drop-in for _native_sgemm_values)."""
+        lib = self._require("spaceslug_q4gemm")
+        if k % 32 or m <= 0 or n <= 0 or k <= 0:
+            raise BackendError("native q4gemm needs m >= 1, n >= 1 and k % 32 == 0")
+        xx = _f32(x, m * k, "x")
+        ww = _u8(w_packed, n * (k // 2), "w_packed")
+        ss = _f32(w_scales, n * (k // 32), "w_scales")
+        yy = np.empty(m * n, dtype=np.float32)
+        self._check(lib.spaceslug_q4gemm(xx.ctypes.data_as(_f32p), ww.ctypes.data_as(_u8p), ss.ctypes.data_as(_f32p),
+                                         yy.ctypes.data_as(_f32p), m, n, k), "q4gemm")
+        return yy.reshape(m, n)
+
+    def q4gemm_lora_values(self, x: Any, w_packed: Any, w_scales: Any, lora_a: Any, lora_b: Any, m: int, n: int,
+                           k: int, rank: int, scale: float) -> np.ndarray:
+        """y = x * dequant(W) + scale * (x * lora_a) * lora_b in one call (spaceslug_q4gemm_lora)."""
+        lib = self._require("spaceslug_q4gemm_lora")
+        if k % 32 or m <= 0 or n <= 0 or k <= 0 or rank <= 0:
+            raise BackendError("native q4gemm_lora needs m, n, rank >= 1 and k % 32 == 0")
+        xx = _f32(x, m * k, "x")
+        ww = _u8(w_packed, n * (k // 2), "w_packed")
+        ss = _f32(w_scales, n * (k // 32), "w_scales")
+        aa = _f32(lora_a, k * rank, "lora_a")
+        bb = _f32(lora_b, rank * n, "lora_b")
+        yy = np.empty(m * n, dtype=np.float32)
+        self._check(lib.spaceslug_q4gemm_lora(xx.ctypes.data_as(_f32p), ww.ctypes.data_as(_u8p),
+                                              ss.ctypes.data_as(_f32p), aa.ctypes.data_as(_f32p),
+                                              bb.ctypes.data_as(_f32p), yy.ctypes.data_as(_f32p), m, n, k, rank,
+                                              float(scale)), "q4gemm_lora")
+        return yy.reshape(m, n)
+
+    def execute_q4gemm_native(self, x: Any, w_packed: Any, w_scales: Any, m: int, n: int, k: int, *,
+                              cpu_reference: Any | None = None, tolerance: float = 1e-5) -> ExecutionResult:
+        started = time.perf_counter()
+        values = self.q4gemm_values(x, w_packed, w_scales, m, n, k)
+        metrics = self._parity(values, cpu_reference, tolerance)
+        metrics["host_elapsed_seconds"] = time.perf_counter() - started
+        return ExecutionResult("ok" if metrics.get("status", "pass") == "pass" else "error", "q4gemm",
+                               "spaceslug-hip", self.runtime_revision, None, False, metrics,
+                               {"m": m, "n": n, "k": k, "values": values})
+
+    def execute_q4gemm_lora_native(self, x: Any, w_packed: Any, w_scales: Any, lora_a: Any, lora_b: Any, m: int,
+                                   n: int, k: int, rank: int, alpha: float, *, cpu_reference: Any | None = None,
+                                   tolerance: float = 1e-5) -> ExecutionResult:
+        """LoRA scale = alpha / rank (lora.py:22)."""
+        values = self.q4gemm_lora_values(x, w_packed, w_scales, lora_a, lora_b, m, n, k, rank, alpha / rank)
+        metrics = self._parity(values, cpu_reference, tolerance)
+        return ExecutionResult("ok" if metrics.get("status", "pass") == "pass" else "error", "q4gemm_lora",
+                               "spaceslug-hip", self.runtime_revision, None, False, metrics,
+                               {"m": m, "n": n, "k": k, "rank": rank, "values": values})
+
+    def create_q4_weight(self, w_packed: Any, w_scales: Any, n: int, k: int) -> Q4Weight:
+        lib = self._require("spaceslug_q4_weight_create")
+        if k % 32 or n <= 0 or k <= 0:
+            raise BackendError("q4 weight needs n >= 1 and k % 32 == 0")
+        ww = _u8(w_packed, n * (k // 2), "w_packed")
+        ss = _f32(w_scales, n * (k // 32), "w_scales")
+        handle = lib.spaceslug_q4_weight_create(ww.ctypes.data_as(_u8p), ss.ctypes.data_as(_f32p), n, k)
+        if not handle:
+            raise BackendError(f"native spaceslug_q4_weight_create failed: {self._last_error()}")
+        return Q4Weight(self, handle, n, k)
+
+    # -- device-pointer entry points (e.g. torch tensors: tensor.data_ptr(), stream.cuda_stream) -----
+    def q4gemm_device(self, d_x: int, d_w_packed: int, d_w_scales: int, d_y: int, m: int, n: int, k: int,
+                      stream: int = 0) -> None:
+        lib = self._require("spaceslug_q4gemm_device")
+        code = lib.spaceslug_q4gemm_device(ctypes.c_void_p(d_x), ctypes.c_void_p(d_w_packed),
+                                           ctypes.c_void_p(d_w_scales), ctypes.c_void_p(d_y), m, n, k,
+                                           ctypes.c_void_p(stream))
+        self._check(code, "q4gemm_device")
+
+    def q4gemm_lora_device(self, d_x: int, d_w_packed: int, d_w_scales: int, d_lora_a: int, d_lora_b: int, d_y: int,
+                           m: int, n: int, k: int, rank: int, scale: float, stream: int = 0) -> None:
+        lib = self._require("spaceslug_q4gemm_lora_device")
+        code = lib.spaceslug_q4gemm_lora_device(ctypes.c_void_p(d_x), ctypes.c_void_p(d_w_packed),
+                                                ctypes.c_void_p(d_w_scales), ctypes.c_void_p(d_lora_a),
+                                                ctypes.c_void_p(d_lora_b), ctypes.c_void_p(d_y), m, n, k, rank,
+                                                float(scale), ctypes.c_void_p(stream))
+        self._check(code, "q4gemm_lora_device")
+
+    # -- helpers -----------------------------------------------------------------------------------
+    @staticmethod
+    def _parity(values: np.ndarray, cpu_reference: Any | None, tolerance: float) -> dict[str, Any]:
+        if cpu_reference is None:
+            return {"parity": "not-run"}
+        ref = np.asarray(cpu_reference, dtype=np.float64)
+        if ref.size != values.size:
+            raise BackendError("CPU reference length does not match GPU output")
+        return {"parity": "cpu-reference", **compare_float_arrays(values, ref, tolerance=tolerance)}

@@ -1,0 +1,275 @@
+"""GPU parity of the int4 GEMM/GEMV against the CPU oracle, through the C-ABI.
+
+Bar: max |gpu - ref| / max(1, |ref|) <= 1e-5 against the double-precision
+reference (the reference's own KAT bar is 1e-3: test_q4gemm.cpp:49). Full-size
+workload shapes are checked on the oracle where it finishes in seconds, on a row
+sample where it does not, and through exact size-independent properties
+(power-of-two scaling, column permutation, zero adapter).
+"""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+from cases import lora_factors, make_case, reference_kat_case
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+REF_TOL = 1e-3
+
+
+def note(msg: str) -> None:
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def check(oracle, got, want, tol=TOL, label=""):
+    rep = oracle.compare(got, want, tol)
+    note(f"{label} max_rel={rep['max_relative_error']:.3e} normwise={rep['normwise_error']:.3e}")
+    assert rep["status"] == "pass", rep
+    return rep
+
+
+def threads():
+    import os
+
+    return min(16, os.cpu_count() or 1)
+
+
+# -- helpers for device-pointer calls ---------------------------------------------------------
+
+def to_dev(a, torch):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
+
+
+def run_device(session, torch, x_t, w_t, s_t, m, n, k, stream=None):
+    y_t = torch.empty((m, n), dtype=torch.float32, device="cuda:0")
+    st = stream if stream is not None else torch.cuda.current_stream()
+    session.q4gemm_device(x_t.data_ptr(), w_t.data_ptr(), s_t.data_ptr(), y_t.data_ptr(), m, n, k, st.cuda_stream)
+    st.synchronize()
+    return y_t
+
+
+# -- small and edge shapes through the synchronous host entry point ---------------------------
+
+def test_tiny_projection_shape(session, oracle, gpu):
+    note("tiny 128x64x64")
+    c = make_case(128, 64, 64)
+    got = session.q4gemm_values(c.x, c.packed, c.scales, 128, 64, 64)
+    check(oracle, got, oracle.q4gemm_ref(c.x, c.b, c.scales), label="tiny")
+
+
+def test_reference_kat_256(session, oracle, gpu):
+    """The reference's KAT (test_q4gemm.cpp:168-176, bar 1e-3 at :49). Its scales are ~1 (not
+    0.01-0.05), so outputs are ~45 and the fp32 group partials are ~30x larger than in the
+    workload configurations: fp32 MFMA accumulation (one rounding per product) gives
+    ~2e-5 here. Held to the reference's bar and to a 3e-5 regression bound."""
+    note("reference KAT 256^3")
+    c = reference_kat_case()
+    got = session.q4gemm_values(c.x, c.packed, c.scales, 256, 256, 256)
+    want = oracle.q4gemm_ref(c.x, c.b, c.scales)
+    check(oracle, got, want, REF_TOL, label="kat@1e-3")
+    check(oracle, got, want, 3e-5, label="kat@3e-5")
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("n,k", [(1, 32), (7, 64), (64, 2080), (333, 4096), (1000, 96)])
+def test_gemv_shapes(session, oracle, gpu, m, n, k):
+    note(f"gemv m={m} n={n} k={k}")
+    c = make_case(m, n, k)
+    got = session.q4gemm_values(c.x, c.packed, c.scales, m, n, k)
+    check(oracle, got, oracle.q4gemm_packed(c.x, c.packed, c.scales), label=f"gemv {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m,n,k", [(5, 1, 32), (5, 17, 96), (16, 256, 256), (17, 300, 1024), (32, 64, 64),
+                                   (33, 129, 160), (100, 300, 512), (130, 260, 1056), (256, 512, 2048)])
+def test_mfma_shapes(session, oracle, gpu, m, n, k):
+    note(f"mfma m={m} n={n} k={k}")
+    c = make_case(m, n, k)
+    got = session.q4gemm_values(c.x, c.packed, c.scales, m, n, k)
+    check(oracle, got, oracle.q4gemm_packed(c.x, c.packed, c.scales, threads=threads()), label=f"mfma {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m", [1, 3, 24])
+def test_extreme_nibbles_and_scales(session, oracle, gpu, m):
+    note(f"extreme values m={m}")
+    n, k = 96, 256
+    c = make_case(m, n, k)
+    b = np.where(np.arange(k * n).reshape(k, n) % 3 == 0, -8, 7).astype(np.int8)
+    b[:, 5] = -8
+    b[:, 6] = 7
+    b[:, 7] = 0
+    scales = c.scales.copy()
+    scales[0, :] = 1e-4
+    scales[1, :] = 100.0
+    packed = oracle.pack_q4(b)
+    got = session.q4gemm_values(c.x, packed, scales, m, n, k)
+    check(oracle, got, oracle.q4gemm_ref(c.x, b, scales), label="extreme")
+    # An all-zero column is exactly 0 on the MFMA path; the decode path subtracts the
+    # offset-binary bias sum(x)/64 and leaves rounding residue of order 2^-24 * sum|x|.
+    assert np.abs(got[:, 7]).max() <= 2.0**-20 * np.abs(c.x).sum(axis=1).max()
+
+
+def test_unit_vectors_select_dequantized_rows(session, oracle, gpu):
+    note("unit vectors")
+    n, k = 40, 128
+    c = make_case(4, n, k)
+    for m in (1, 4, 8):
+        ks = [0, 31, 64, 127, 5, 33, 90, 100][:m]
+        x = np.zeros((m, k), np.float32)
+        for r, kk in enumerate(ks):
+            x[r, kk] = 1.0
+        got = session.q4gemm_values(x, c.packed, c.scales, m, n, k)
+        for r, kk in enumerate(ks):
+            want = c.b[kk, :].astype(np.float32) * c.scales[:, kk // 32]
+            assert np.array_equal(got[r], want), (m, r, kk)
+
+
+def test_deterministic_repeat(session, oracle, gpu):
+    note("determinism")
+    for m, n, k in ((1, 500, 1024), (16, 512, 1024), (64, 256, 512)):
+        c = make_case(m, n, k)
+        a = session.q4gemm_values(c.x, c.packed, c.scales, m, n, k)
+        b = session.q4gemm_values(c.x, c.packed, c.scales, m, n, k)
+        assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("m,n,k,rank", [(1, 64, 64, 4), (3, 100, 96, 1), (64, 64, 64, 8), (40, 200, 256, 16),
+                                        (130, 96, 512, 17), (16, 128, 128, 64)])
+def test_lora_shapes(session, oracle, gpu, m, n, k, rank):
+    note(f"lora m={m} n={n} k={k} r={rank}")
+    c = make_case(m, n, k)
+    la, lb = lora_factors(k, n, rank)
+    scale = 32.0 / rank
+    got = session.q4gemm_lora_values(c.x, c.packed, c.scales, la, lb, m, n, k, rank, scale)
+    want = oracle.q4gemm_lora(c.x, c.packed, c.scales, la, lb, scale, threads=threads())
+    check(oracle, got, want, label="lora")
+
+
+def test_lora_reference_kat_style(session, oracle, gpu):
+    # tests/test_lora_delta_api.cpp:9-18 inputs (sin/cos) through the fused path with a zero base.
+    note("lora sin/cos")
+    m, rank, h = 3, 4, 64
+    x = np.sin(np.arange(m * h, dtype=np.float32) * np.float32(0.07)).astype(np.float32)
+    a = (np.cos(np.arange(h * rank, dtype=np.float32) * np.float32(0.11)) * np.float32(0.1)).astype(np.float32)
+    b = (np.sin(np.arange(rank * h, dtype=np.float32) * np.float32(0.13)) * np.float32(0.1)).astype(np.float32)
+    packed = np.zeros((h, h // 2), np.uint8)
+    scales = np.ones((h, h // 32), np.float32)
+    got = session.q4gemm_lora_values(x, packed, scales, a, b, m, h, h, rank, 1.0)
+    ref = (x.reshape(m, h).astype(np.float64) @ a.reshape(h, rank).astype(np.float64)) @ b.reshape(rank, h).astype(
+        np.float64)
+    assert np.max(np.abs(got - ref)) <= 2e-4  # the reference test's bar
+    check(oracle, got, ref, label="lora sin/cos")
+
+
+def test_weight_handle(session, oracle, gpu):
+    note("weight handle")
+    n, k = 300, 512
+    c = make_case(8, n, k)
+    with session.create_q4_weight(c.packed, c.scales, n, k) as w:
+        for m in (1, 4, 8):
+            x = c.x[:m]
+            check(oracle, w.run(x, m), oracle.q4gemm_packed(x, c.packed, c.scales), label=f"handle m={m}")
+
+
+def test_sgemm(session, gpu):
+    note("sgemm")
+    rng = np.random.default_rng(0)
+    for m, n, k in ((64, 64, 32), (128, 192, 64), (192, 64, 256)):
+        a = rng.standard_normal((m, k)).astype(np.float32)
+        b = rng.standard_normal((k, n)).astype(np.float32)
+        got = session.sgemm_values(a, b, m, n, k)
+        ref = a.astype(np.float64) @ b.astype(np.float64)
+        rel = np.abs(got - ref) / np.maximum(1.0, np.abs(ref))
+        # single fp32 accumulator over K, like the reference shader; bar of parity.py:6 (1e-3)
+        assert rel.max() <= 1e-4
+
+
+# -- workload shapes (device pointers, inputs resident in HBM) --------------------------------
+
+def test_decode_gemv_m1_k4096_n14336(session, oracle, gpu):
+    import torch
+
+    m, n, k = 1, 14336, 4096
+    note(f"gemv {m}x{k}x{n}, 3 distinct weight copies")
+    for copy in range(3):
+        c = make_case(m, n, k, seed_b=0x9ABCDEF0 + copy, seed_s=0x13579BDF + copy, seed_a=0x12345678 + copy)
+        y = run_device(session, torch, to_dev(c.x, torch), to_dev(c.packed, torch), to_dev(c.scales, torch), m, n, k)
+        check(oracle, y.cpu().numpy(), oracle.q4gemm_packed(c.x, c.packed, c.scales, threads=threads()),
+              label=f"C2 copy {copy}")
+
+
+def test_small_batch_m16_k4096_n4096(session, oracle, gpu):
+    import torch
+
+    m, n, k = 16, 4096, 4096
+    note(f"m={m} k={k} n={n}")
+    c = make_case(m, n, k)
+    y = run_device(session, torch, to_dev(c.x, torch), to_dev(c.packed, torch), to_dev(c.scales, torch), m, n, k)
+    check(oracle, y.cpu().numpy(), oracle.q4gemm_packed(c.x, c.packed, c.scales, threads=threads()), label="C3")
+
+
+def test_prefill_m2048_k4096_n14336(session, oracle, gpu):
+    import torch
+
+    m, n, k = 2048, 14336, 4096
+    note(f"prefill {m}x{k}x{n}")
+    c = make_case(m, n, k)
+    x_t, w_t, s_t = to_dev(c.x, torch), to_dev(c.packed, torch), to_dev(c.scales, torch)
+    y = run_device(session, torch, x_t, w_t, s_t, m, n, k).cpu().numpy()
+    rows = sorted({0, 1, 15, 16, 127, 128, 1023, 1024, 2046, 2047} | set(range(600, 606)))
+    want = np.concatenate([oracle.q4gemm_packed(c.x, c.packed, c.scales, rows=(r, r + 1), threads=threads())
+                           for r in rows])
+    check(oracle, y[rows], want, label="C4 row sample")
+    note("prefill: x*2 -> y*2 exactly")
+    y2 = run_device(session, torch, x_t * 2, w_t, s_t, m, n, k).cpu().numpy()
+    assert np.array_equal(y2, 2 * y)
+    note("prefill: column permutation")
+    perm = torch.randperm(n, generator=torch.Generator().manual_seed(1))
+    yp = run_device(session, torch, x_t, w_t[perm.to("cuda:0")].contiguous(), s_t[perm.to("cuda:0")].contiguous(),
+                    m, n, k).cpu().numpy()
+    assert np.array_equal(yp, y[:, perm.numpy()])
+
+
+def test_lora_m512_k4096_n4096_r16(session, oracle, gpu):
+    import torch
+
+    m, n, k, rank, alpha = 512, 4096, 4096, 16, 32.0
+    note(f"lora {m}x{k}x{n} r={rank}")
+    c = make_case(m, n, k)
+    la, lb = lora_factors(k, n, rank)
+    x_t, w_t, s_t = to_dev(c.x, torch), to_dev(c.packed, torch), to_dev(c.scales, torch)
+    la_t, lb_t = to_dev(la, torch), to_dev(lb, torch)
+    y_t = torch.empty((m, n), dtype=torch.float32, device="cuda:0")
+    st = torch.cuda.current_stream()
+    session.q4gemm_lora_device(x_t.data_ptr(), w_t.data_ptr(), s_t.data_ptr(), la_t.data_ptr(), lb_t.data_ptr(),
+                               y_t.data_ptr(), m, n, k, rank, alpha / rank, st.cuda_stream)
+    st.synchronize()
+    y = y_t.cpu().numpy()
+    rows = [0, 1, 63, 64, 255, 256, 510, 511]
+    want = np.concatenate([oracle.q4gemm_lora(c.x, c.packed, c.scales, la, lb, alpha / rank, rows=(r, r + 1),
+                                              threads=threads()) for r in rows])
+    check(oracle, y[rows], want, label="C5 row sample")
+    note("lora: zero adapter equals the base projection exactly")
+    z_t = torch.zeros_like(la_t)
+    session.q4gemm_lora_device(x_t.data_ptr(), w_t.data_ptr(), s_t.data_ptr(), z_t.data_ptr(), lb_t.data_ptr(),
+                               y_t.data_ptr(), m, n, k, rank, alpha / rank, st.cuda_stream)
+    st.synchronize()
+    base = run_device(session, torch, x_t, w_t, s_t, m, n, k)
+    assert torch.equal(y_t, base)
+
+
+def test_device_entry_on_side_stream(session, oracle, gpu):
+    import torch
+
+    m, n, k = 2, 1024, 1024
+    note("side stream")
+    c = make_case(m, n, k)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        x_t, w_t, s_t = to_dev(c.x, torch), to_dev(c.packed, torch), to_dev(c.scales, torch)
+    y = run_device(session, torch, x_t, w_t, s_t, m, n, k, stream=s)
+    check(oracle, y.cpu().numpy(), oracle.q4gemm_packed(c.x, c.packed, c.scales), label="side stream")
