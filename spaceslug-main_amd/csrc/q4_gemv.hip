@@ -267,7 +267,7 @@ __device__ __forceinline__ float pipe_column(const PipeSlot<SPC, D>& slot, const
     return wave_reduce_dpp(acc);
 }
 
-template <int SPC, int D, bool STRIDED>
+template <int SPC, int D>
 __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float* x,  // not restrict: see issue_chunk
                                                                    const u32x4* __restrict__ wq,
                                                                    const float* __restrict__ ws,
@@ -279,11 +279,9 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
     const int lane = threadIdx.x & 63;
     const int wave =
         __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)));
+    // Each wavefront streams one contiguous run of columns (a grid-strided
+    // assignment, all wavefronts sweeping one band together, measured slower).
     const int cpb = D * iters;  // columns per wavefront (<= 64)
-    const int nwaves = static_cast<int>(gridDim.x * (blockDim.x >> 6));
-    // Column of the wavefront's i-th step: contiguous runs per wavefront, or
-    // grid-strided so that at step i all wavefronts together read one band.
-    auto column = [&](int i) { return STRIDED ? i * nwaves + wave : wave * cpb + i; };
     const int col0 = wave * cpb;
     const int G = K >> 5;
 
@@ -307,7 +305,7 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
     PipeSlot<SPC, D> slot[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-        pipe_issue<SPC, D>(slot[d], wq, ws, column(d), N, G, off16, off4);
+        pipe_issue<SPC, D>(slot[d], wq, ws, col0 + d, N, G, off16, off4);
         // slot by slot, as in the steady state, so the loop's load counts line up
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -343,12 +341,8 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
 #pragma unroll
         for (int d = 0; d < D; ++d, ++i) {
             const float t = pipe_column<SPC, D>(slot[d], xv, cr, valid);
-            if (STRIDED) {
-                if (lane == 0 && column(i) < N) y[column(i)] = t * kE4m3OffsetUnit;
-            } else {
-                result = lane == i ? t : result;
-            }
-            pipe_issue<SPC, D>(slot[d], wq, ws, column(i + D), N, G, off16, off4);
+            result = lane == i ? t : result;
+            pipe_issue<SPC, D>(slot[d], wq, ws, col0 + i + D, N, G, off16, off4);
             // Keep the next slot's arithmetic below this refill: otherwise the scheduler
             // interleaves slots and must wait for every outstanding load first.
             __builtin_amdgcn_sched_barrier(0);
@@ -357,13 +351,10 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
 #pragma unroll
     for (int d = 0; d < D; ++d, ++i) {
         const float t = pipe_column<SPC, D>(slot[d], xv, cr, valid);
-        if (STRIDED) {
-            if (lane == 0 && column(i) < N) y[column(i)] = t * kE4m3OffsetUnit;
-        } else {
-            result = lane == i ? t : result;
-        }
+        result = lane == i ? t : result;
     }
-    if (!STRIDED && lane < cpb && col0 + lane < N) y[col0 + lane] = result * kE4m3OffsetUnit;
+    // lane c holds column col0 + c: one coalesced store of the wavefront's run
+    if (lane < cpb && col0 + lane < N) y[col0 + lane] = result * kE4m3OffsetUnit;
 }
 
 template <int M, int SPC, int CPW>
@@ -386,11 +377,31 @@ hipError_t launch_rows(const float* x, const uint8_t* w_packed, const float* w_s
 
 }  // namespace
 
+// Single-row decode with K <= 4096: the pipelined kernel, D = 4 columns in flight
+// per wavefront and about 3.5 wavefronts per CU (measured best on MI355X for
+// K = 4096, N = 14336 among D in 1..8 and 896..14336 wavefronts).
+static hipError_t launch_gemv_pipelined(const DeviceInfo& dev, const float* x, const uint8_t* w_packed,
+                                 const float* w_scales, float* y, uint32_t n, uint32_t k, hipStream_t stream) {
+    constexpr int D = 4;
+    const size_t target_waves = static_cast<size_t>(dev.cu_count) * 7 / 2;
+    size_t iters = (static_cast<size_t>(n) + target_waves * D - 1) / (target_waves * D);
+    if (iters < 1) iters = 1;
+    if (iters > 64 / D) iters = 64 / D;
+    const size_t cpb = D * iters;
+    const size_t waves = (static_cast<size_t>(n) + cpb - 1) / cpb;
+    const size_t blocks = (waves + kGemvThreads / 64 - 1) / (kGemvThreads / 64);
+    hipLaunchKernelGGL((q4_gemv_pipe_kernel<2, D>), dim3(static_cast<unsigned>(blocks)), dim3(kGemvThreads), 0,
+                       stream, x, reinterpret_cast<const u32x4*>(w_packed), w_scales, y, static_cast<int>(n),
+                       static_cast<int>(k), static_cast<int>(iters));
+    return hipGetLastError();
+}
+
 hipError_t launch_gemv(const DeviceInfo& dev, const float* x, const uint8_t* w_packed, const float* w_scales,
                        float* y, uint32_t m, uint32_t n, uint32_t k, hipStream_t stream) {
-    (void)dev;
     switch (m) {
-        case 1: return launch_rows<1, 2, 8>(x, w_packed, w_scales, y, n, k, stream);
+        case 1:
+            if (k / kGroup <= 128) return launch_gemv_pipelined(dev, x, w_packed, w_scales, y, n, k, stream);
+            return launch_rows<1, 2, 8>(x, w_packed, w_scales, y, n, k, stream);
         case 2: return launch_rows<2, 2, 4>(x, w_packed, w_scales, y, n, k, stream);
         case 3: return launch_rows<3, 1, 4>(x, w_packed, w_scales, y, n, k, stream);
         case 4: return launch_rows<4, 1, 4>(x, w_packed, w_scales, y, n, k, stream);
