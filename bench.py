@@ -182,6 +182,9 @@ def main() -> int:
     ap.add_argument("--graph", action="store_true", help="replay the 64-launch sweep as one HIP graph")
     ap.add_argument("--gemv-only", action="store_true", help="skip the secondary GEMM configurations")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget (0 disables)")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="first run 3 plain device copies of this many MiB (a known-traffic kernel for scaling "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the int4 path is measured "
@@ -197,6 +200,16 @@ def main() -> int:
 
     session = BackendSession()
     session.capability()  # fails loudly when the HIP library is missing
+
+    if args.copy_calibration_mib > 0:
+        n = args.copy_calibration_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"[bench] copy calibration: 3 x {args.copy_calibration_mib} MiB read + write", file=sys.stderr, flush=True)
+        del src, dst
 
     print(f"[bench] gemv sweep steps={args.steps} warmup={args.warmup} graph={args.graph}", file=sys.stderr,
           flush=True)

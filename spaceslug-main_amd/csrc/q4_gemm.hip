@@ -14,16 +14,17 @@
 //     acc += (double)s * P. Scale application moves out of the inner loop, and
 //     the long K sum is carried in double, which keeps the max relative error
 //     against the double-precision reference well under 1e-5 at K = 4096;
-//   - operands of group g+1 are loaded while group g computes (register
-//     double buffering); A rows and weight columns go global -> VGPR through
-//     L1/L2 with no LDS round trip;
+//   - operands of the next PD groups are in flight while a group computes (a
+//     ring of register buffers); A rows and weight columns go global -> VGPR
+//     through L1/L2 with no LDS round trip;
 //   - large grids are XCD-aware: workgroup ids are remapped so each of the 8
 //     XCDs (one L2 each) walks a contiguous band of output tiles, sharing A
 //     rows and weight columns within its L2;
 //   - when the grid is too small to fill 256 CUs, K is split across
-//     blockIdx.z and a second kernel sums the partials in a fixed order.
-// The fused LoRA epilogue adds scale * T[rows] * lb[:, cols] with T = x * la
-// precomputed by lora_t_kernel, using the same MFMA tile layout (r in the K slot).
+//     blockIdx.y and a second kernel sums the partials in a fixed order.
+// LoRA: lora_t_kernel computes T = x * la on the MFMA as K-split partials; the
+// GEMM epilogue sums them and adds scale * T[rows] * lb[:, cols] with the same
+// MFMA tile layout (r in the K slot), before the single store of y.
 #include "q4_device.hpp"
 #include "q4_kernels.hpp"
 
@@ -53,11 +54,36 @@ __device__ __forceinline__ void xcd_tile(int tiles_m, int tiles_n, int& tm, int&
     tn = lin / tiles_m;
 }
 
-template <int WM, int WN, int WAVES_M, int WAVES_N>
+// Operands of one 32-value group for a wavefront's WM x WN tiles.
+template <int WM, int WN>
+struct GroupOps {
+    f32x4 alo[WM], ahi[WM];  // x[row j][8q .. 8q+7] of each M tile
+    uint32_t bw[WN];         // packed word q of column j's group, each N tile
+    float bs[WN];            // scale of column j's group, each N tile
+};
+
+template <int WM, int WN>
+__device__ __forceinline__ void load_group(GroupOps<WM, WN>& o, const float* const (&arow)[WM],
+                                           const uint32_t* const (&bcol)[WN], const float* const (&scol)[WN], int g) {
+#pragma unroll
+    for (int tm = 0; tm < WM; ++tm) {
+        o.alo[tm] = *reinterpret_cast<const f32x4*>(arow[tm] + g * 32);
+        o.ahi[tm] = *reinterpret_cast<const f32x4*>(arow[tm] + g * 32 + 4);
+    }
+#pragma unroll
+    for (int tn = 0; tn < WN; ++tn) {
+        o.bw[tn] = bcol[tn][g * 4];
+        o.bs[tn] = scol[tn][g];
+    }
+}
+
+template <int WM, int WN, int WAVES_M, int WAVES_N, int PD>
+// x, wq and ws are deliberately not __restrict__: as provably invariant loads
+// the compiler would be free to re-issue the prefetched group's loads at their
+// use (to save registers), which serialises them behind the compute.
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void q4_gemm_mfma_kernel(
-    const float* __restrict__ x, const uint32_t* __restrict__ wq, const float* __restrict__ ws,
-    float* __restrict__ out, int M, int N, int K, int tiles_m, int tiles_n, int groups_per_split,
-    const float* __restrict__ lt, const float* __restrict__ lb, int R, float lscale) {
+    const float* x, const uint32_t* wq, const float* ws, float* __restrict__ out, int M, int N, int K, int tiles_m, int tiles_n, int groups_per_split,
+    const float* __restrict__ tpart, int t_splits, const float* __restrict__ lb, int R, float lscale) {
     using Shape = TileShape<WM, WN, WAVES_M, WAVES_N>;
     const int lane = threadIdx.x & 63;
     const int wid = threadIdx.x >> 6;
@@ -97,50 +123,18 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void q4_gemm_mfma_kernel(
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[tm][tn][i] = 0.0;
 
-    float4 alo[WM], ahi[WM];
-    uint32_t bw[WN];
-    float bs[WN];
-    if (g_begin < g_end) {
-#pragma unroll
-        for (int tm = 0; tm < WM; ++tm) {
-            alo[tm] = *reinterpret_cast<const float4*>(arow[tm] + g_begin * 32);
-            ahi[tm] = *reinterpret_cast<const float4*>(arow[tm] + g_begin * 32 + 4);
-        }
-#pragma unroll
-        for (int tn = 0; tn < WN; ++tn) {
-            bw[tn] = bcol[tn][g_begin * 4];
-            bs[tn] = scol[tn][g_begin];
-        }
-    }
-
     const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int g = g_begin; g < g_end; ++g) {
-        const int gn = min(g + 1, g_end - 1);
-        float4 alo_n[WM], ahi_n[WM];
-        uint32_t bw_n[WN];
-        float bs_n[WN];
-#pragma unroll
-        for (int tm = 0; tm < WM; ++tm) {
-            alo_n[tm] = *reinterpret_cast<const float4*>(arow[tm] + gn * 32);
-            ahi_n[tm] = *reinterpret_cast<const float4*>(arow[tm] + gn * 32 + 4);
-        }
-#pragma unroll
-        for (int tn = 0; tn < WN; ++tn) {
-            bw_n[tn] = bcol[tn][gn * 4];
-            bs_n[tn] = scol[tn][gn];
-        }
-
+    // One group: P = x * v over 32 K values on the MFMA from zero, then acc += s * P.
+    auto do_group = [&](const GroupOps<WM, WN>& o) {
         f32x4 P[WM][WN];
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             float bv[WN];
 #pragma unroll
-            for (int tn = 0; tn < WN; ++tn) bv[tn] = nibble_signed(bw[tn], t);
+            for (int tn = 0; tn < WN; ++tn) bv[tn] = nibble_signed(o.bw[tn], t);
 #pragma unroll
             for (int tm = 0; tm < WM; ++tm) {
-                const float av = t == 0 ? alo[tm].x : t == 1 ? alo[tm].y : t == 2 ? alo[tm].z
-                               : t == 3 ? alo[tm].w : t == 4 ? ahi[tm].x : t == 5 ? ahi[tm].y
-                               : t == 6 ? ahi[tm].z : ahi[tm].w;
+                const float av = t < 4 ? o.alo[tm][t & 3] : o.ahi[tm][t & 3];
 #pragma unroll
                 for (int tn = 0; tn < WN; ++tn)
                     P[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[tn], t == 0 ? zero : P[tm][tn], 0, 0, 0);
@@ -148,26 +142,111 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void q4_gemm_mfma_kernel(
         }
 #pragma unroll
         for (int tn = 0; tn < WN; ++tn) {
-            const double s = static_cast<double>(bs[tn]);
+            const double sc = static_cast<double>(o.bs[tn]);
 #pragma unroll
             for (int tm = 0; tm < WM; ++tm)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) acc[tm][tn][i] = fma(s, static_cast<double>(P[tm][tn][i]), acc[tm][tn][i]);
+                for (int i = 0; i < 4; ++i) acc[tm][tn][i] = fma(sc, static_cast<double>(P[tm][tn][i]), acc[tm][tn][i]);
         }
+    };
+    if (g_begin < g_end) {
+        if constexpr (PD == 1) {
+            // Double buffer in plain register arrays: issue group g+1 into the *_n
+            // registers, compute group g, then take them over (with 16*WM*WN MFMAs
+            // per group the loads have landed by then).
+            f32x4 alo[WM], ahi[WM];
+            uint32_t bw[WN];
+            float bs[WN];
 #pragma unroll
-        for (int tm = 0; tm < WM; ++tm) {
-            alo[tm] = alo_n[tm];
-            ahi[tm] = ahi_n[tm];
-        }
+            for (int tm = 0; tm < WM; ++tm) {
+                alo[tm] = *reinterpret_cast<const f32x4*>(arow[tm] + g_begin * 32);
+                ahi[tm] = *reinterpret_cast<const f32x4*>(arow[tm] + g_begin * 32 + 4);
+            }
 #pragma unroll
-        for (int tn = 0; tn < WN; ++tn) {
-            bw[tn] = bw_n[tn];
-            bs[tn] = bs_n[tn];
+            for (int tn = 0; tn < WN; ++tn) {
+                bw[tn] = bcol[tn][g_begin * 4];
+                bs[tn] = scol[tn][g_begin];
+            }
+            for (int g = g_begin; g < g_end; ++g) {
+                const int gn = min(g + 1, g_end - 1);
+                f32x4 alo_n[WM], ahi_n[WM];
+                uint32_t bw_n[WN];
+                float bs_n[WN];
+#pragma unroll
+                for (int tm = 0; tm < WM; ++tm) {
+                    alo_n[tm] = *reinterpret_cast<const f32x4*>(arow[tm] + gn * 32);
+                    ahi_n[tm] = *reinterpret_cast<const f32x4*>(arow[tm] + gn * 32 + 4);
+                }
+#pragma unroll
+                for (int tn = 0; tn < WN; ++tn) {
+                    bw_n[tn] = bcol[tn][gn * 4];
+                    bs_n[tn] = scol[tn][gn];
+                }
+                f32x4 P[WM][WN];
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    float bv[WN];
+#pragma unroll
+                    for (int tn = 0; tn < WN; ++tn) bv[tn] = nibble_signed(bw[tn], t);
+#pragma unroll
+                    for (int tm = 0; tm < WM; ++tm) {
+                        const float av = t < 4 ? alo[tm][t & 3] : ahi[tm][t & 3];
+#pragma unroll
+                        for (int tn = 0; tn < WN; ++tn)
+                            P[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[tn], t == 0 ? zero : P[tm][tn], 0,
+                                                                             0, 0);
+                    }
+                }
+#pragma unroll
+                for (int tn = 0; tn < WN; ++tn) {
+                    const double sc = static_cast<double>(bs[tn]);
+#pragma unroll
+                    for (int tm = 0; tm < WM; ++tm)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            acc[tm][tn][i] = fma(sc, static_cast<double>(P[tm][tn][i]), acc[tm][tn][i]);
+                }
+#pragma unroll
+                for (int tm = 0; tm < WM; ++tm) {
+                    alo[tm] = alo_n[tm];
+                    ahi[tm] = ahi_n[tm];
+                }
+#pragma unroll
+                for (int tn = 0; tn < WN; ++tn) {
+                    bw[tn] = bw_n[tn];
+                    bs[tn] = bs_n[tn];
+                }
+            }
+        } else {
+            // PD + 1 buffers used in rotation: while buffer s computes group g+s,
+            // buffer (s+PD) % (PD+1) receives group g+s+PD, so PD groups are in flight
+            // behind the one being computed. The rotation is unrolled, so no buffer
+            // is copied (a register copy would wait for its loads). Loads past the
+            // split are clamped to its last group and never accumulated.
+            constexpr int NB = PD + 1;
+            GroupOps<WM, WN> buf[NB];
+#pragma unroll
+            for (int p = 0; p < PD; ++p) {
+                load_group<WM, WN>(buf[p], arow, bcol, scol, min(g_begin + p, g_end - 1));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            for (int g = g_begin; g < g_end; g += NB) {
+#pragma unroll
+                for (int sl = 0; sl < NB; ++sl) {
+                    load_group<WM, WN>(buf[(sl + PD) % NB], arow, bcol, scol, min(g + sl + PD, g_end - 1));
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (g + sl < g_end) do_group(buf[sl]);  // uniform across the workgroup
+                    // keep the next slot's loads and work below this point so each slot
+                    // waits only for its own loads
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
         }
     }
 
     if (lb != nullptr && blockIdx.y == 0) {
-        // LoRA epilogue: + lscale * T[m0.., :R] * lb[:R, n0..] on the MFMA, r in the K slot.
+        // LoRA epilogue: + lscale * T[m0.., :R] * lb[:R, n0..] on the MFMA, r in the K slot,
+        // with T = sum over the t_splits partials of lora_t_kernel.
 #pragma unroll
         for (int tm = 0; tm < WM; ++tm) {
             const int row = min(m0 + 16 * tm + j, M - 1);
@@ -177,7 +256,11 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void q4_gemm_mfma_kernel(
                 f32x4 P = zero;
                 for (int r0 = 0; r0 < R; r0 += 4) {
                     const int r = r0 + q;
-                    const float av = r < R ? lt[static_cast<size_t>(row) * R + r] : 0.0f;
+                    float av = 0.0f;
+                    if (r < R) {
+                        for (int s = 0; s < t_splits; ++s)
+                            av += tpart[(static_cast<size_t>(s) * M + row) * R + r];
+                    }
                     const float bv = r < R ? lb[static_cast<size_t>(r) * N + col] : 0.0f;
                     P = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, P, 0, 0, 0);
                 }
@@ -203,35 +286,54 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void q4_gemm_mfma_kernel(
     }
 }
 
-// T[m][r] = sum_k x[m][k] * la[k][r], accumulated in double. Grid (M, ceil(R/16)).
-__global__ __launch_bounds__(256) void lora_t_kernel(const float* __restrict__ x,
-                                                     const float* __restrict__ la,
-                                                     float* __restrict__ t, int K, int R) {
-    __shared__ double part[4][16];
-    const int row = blockIdx.x;
+// LoRA pre-pass on the MFMA: tpart[s][m][r] = sum over the groups of split s of
+// x[m][k] * la[k][r] (la is K x R row-major). One wavefront per 16 x 16 tile of
+// (rows, ranks) and split; all of the split's operands are loaded before the
+// first MFMA. Grid (ceil(M/16), ceil(R/16), t_splits).
+constexpr int kLoraGroupsPerWave = 8;
+
+__global__ __launch_bounds__(64) void lora_t_kernel(const float* __restrict__ x, const float* __restrict__ la,
+                                                    float* __restrict__ tpart, int M, int K, int R) {
+    const int lane = threadIdx.x & 63;
+    const int j = lane & 15;
+    const int q = lane >> 4;
+    const int G = K >> 5;
+    const int m0 = blockIdx.x * 16;
     const int r0 = blockIdx.y * 16;
-    double acc[16];
+    const int g_begin = blockIdx.z * kLoraGroupsPerWave;
+    const int row = min(m0 + j, M - 1);
+    const int r = r0 + j;
+    const int rc = min(r, R - 1);
+    const float* xr = x + static_cast<size_t>(row) * K + 8 * q;
+
+    f32x4 a_lo[kLoraGroupsPerWave], a_hi[kLoraGroupsPerWave];
+    float b[kLoraGroupsPerWave][8];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[i] = 0.0;
-    const float* xr = x + static_cast<size_t>(row) * K;
-    for (int k = threadIdx.x; k < K; k += blockDim.x) {
-        const double xv = static_cast<double>(xr[k]);
-        const float* lr = la + static_cast<size_t>(k) * R + r0;
+    for (int i = 0; i < kLoraGroupsPerWave; ++i) {
+        const int g = min(g_begin + i, G - 1);
+        a_lo[i] = *reinterpret_cast<const f32x4*>(xr + g * 32);
+        a_hi[i] = *reinterpret_cast<const f32x4*>(xr + g * 32 + 4);
+        const float* lr = la + static_cast<size_t>(g * 32 + 8 * q) * R + rc;
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-            if (r0 + i < R) acc[i] = fma(xv, static_cast<double>(lr[i]), acc[i]);
+        for (int t = 0; t < 8; ++t) b[i][t] = lr[static_cast<size_t>(t) * R];
     }
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const double v = wave_sum(acc[i]);
-        if (lane == 0) part[wid][i] = v;
+    for (int i = 0; i < kLoraGroupsPerWave; ++i) {
+        if (g_begin + i < G) {  // uniform
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const float av = t < 4 ? a_lo[i][t & 3] : a_hi[i][t & 3];
+                const float bv = r < R ? b[i][t] : 0.0f;
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
+            }
+        }
     }
-    __syncthreads();
-    if (threadIdx.x < 16 && r0 + static_cast<int>(threadIdx.x) < R) {
-        const int i = threadIdx.x;
-        t[static_cast<size_t>(row) * R + r0 + i] =
-            static_cast<float>((part[0][i] + part[1][i]) + (part[2][i] + part[3][i]));
+    float* dst = tpart + static_cast<size_t>(blockIdx.z) * M * R;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int rr = m0 + 4 * q + i;
+        if (rr < M && r < R) dst[static_cast<size_t>(rr) * R + r] = acc[i];
     }
 }
 
@@ -247,34 +349,38 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
     }
 }
 
-template <int WM, int WN, int WAVES_M, int WAVES_N>
+template <int WM, int WN, int WAVES_M, int WAVES_N, int PD>
 hipError_t launch_mfma(const float* x, const uint8_t* w_packed, const float* w_scales, float* out,
-                       uint32_t m, uint32_t n, uint32_t k, int splits, const float* lt,
+                       uint32_t m, uint32_t n, uint32_t k, int splits, const float* tpart, int t_splits,
                        const float* lb, uint32_t rank, float lscale, hipStream_t stream) {
     using Shape = TileShape<WM, WN, WAVES_M, WAVES_N>;
     const int tiles_m = static_cast<int>((m + Shape::kBM - 1) / Shape::kBM);
     const int tiles_n = static_cast<int>((n + Shape::kBN - 1) / Shape::kBN);
     const int G = static_cast<int>(k / kGroup);
     const int gps = (G + splits - 1) / splits;
-    hipLaunchKernelGGL((q4_gemm_mfma_kernel<WM, WN, WAVES_M, WAVES_N>),
+    hipLaunchKernelGGL((q4_gemm_mfma_kernel<WM, WN, WAVES_M, WAVES_N, PD>),
                        dim3(tiles_m * tiles_n, splits), dim3(Shape::kThreads), 0, stream, x,
                        reinterpret_cast<const uint32_t*>(w_packed), w_scales, out,
                        static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), tiles_m,
-                       tiles_n, gps, lt, lb, static_cast<int>(rank), lscale);
+                       tiles_n, gps, tpart, t_splits, lb, static_cast<int>(rank), lscale);
     return hipGetLastError();
 }
 
 // Tile shapes: skinny = one 16-row MFMA tile x 256 columns per workgroup
-// (4 waves of 16 x 64); wide = 128 x 128 per workgroup (2 x 2 waves of 64 x 64).
+// (4 waves of 16 x 64), 4 groups in flight; wide = 128 x 128 per workgroup
+// (2 x 2 waves of 64 x 64), 1 group in flight (register bound: 128 double
+// accumulators + 64 MFMA accumulators per lane).
 using SkinnyShape = TileShape<1, 4, 1, 4>;
+constexpr int kSkinnyPD = 4;
 using WideShape = TileShape<4, 4, 2, 2>;
+constexpr int kWidePD = 1;
 
 size_t align_up(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
 }  // namespace
 
 Q4Plan plan_q4gemm(const DeviceInfo& dev, uint32_t m, uint32_t n, uint32_t k, uint32_t rank) {
-    Q4Plan plan{Q4Plan::kGemv, 1, 0};
+    Q4Plan plan{Q4Plan::kGemv, 1, 0, 0};
     if (rank == 0 && m <= static_cast<uint32_t>(kGemvMaxRows)) {
         return plan;
     }
@@ -294,15 +400,19 @@ Q4Plan plan_q4gemm(const DeviceInfo& dev, uint32_t m, uint32_t n, uint32_t k, ui
     const size_t waves = tiles * waves_per_tile;
     const size_t target = static_cast<size_t>(8) * dev.cu_count;  // two waves per SIMD
     const int groups = static_cast<int>(k / kGroup);
+    const int min_groups = plan.kind == Q4Plan::kMfmaSkinny ? 8 : 4;
     int splits = 1;
-    while (waves * splits * 2 <= target && groups / (splits * 2) >= 4) splits *= 2;
+    while (waves * splits * 2 <= target && groups / (splits * 2) >= min_groups) splits *= 2;
     // Re-derive so that no split is empty.
     const int gps = (groups + splits - 1) / splits;
     splits = (groups + gps - 1) / gps;
     plan.splits = splits;
     size_t bytes = 0;
     if (splits > 1) bytes += align_up(static_cast<size_t>(splits) * m * n * sizeof(float));
-    if (rank > 0) bytes += align_up(static_cast<size_t>(m) * rank * sizeof(float));
+    if (rank > 0) {
+        plan.t_splits = (groups + kLoraGroupsPerWave - 1) / kLoraGroupsPerWave;
+        bytes += align_up(static_cast<size_t>(plan.t_splits) * m * rank * sizeof(float));
+    }
     plan.workspace_bytes = bytes;
     return plan;
 }
@@ -319,22 +429,23 @@ hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float*
         partial = reinterpret_cast<float*>(wsp);
         wsp += align_up(static_cast<size_t>(plan.splits) * m * n * sizeof(float));
     }
-    float* t = nullptr;
+    float* tpart = nullptr;
     if (rank > 0) {
-        t = reinterpret_cast<float*>(wsp);
-        hipLaunchKernelGGL(lora_t_kernel, dim3(m, (rank + 15) / 16), dim3(256), 0, stream, x, la, t,
-                           static_cast<int>(k), static_cast<int>(rank));
+        tpart = reinterpret_cast<float*>(wsp);
+        hipLaunchKernelGGL(lora_t_kernel, dim3((m + 15) / 16, (rank + 15) / 16, plan.t_splits), dim3(64), 0, stream,
+                           x, la, tpart, static_cast<int>(m), static_cast<int>(k), static_cast<int>(rank));
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
     float* out = plan.splits > 1 ? partial : y;
+    const float* lbp = rank ? lb : nullptr;
     hipError_t e;
     if (plan.kind == Q4Plan::kMfmaSkinny) {
-        e = launch_mfma<1, 4, 1, 4>(x, w_packed, w_scales, out, m, n, k, plan.splits, t, rank ? lb : nullptr,
-                                    rank, lora_scale, stream);
+        e = launch_mfma<1, 4, 1, 4, kSkinnyPD>(x, w_packed, w_scales, out, m, n, k, plan.splits, tpart, plan.t_splits,
+                                               lbp, rank, lora_scale, stream);
     } else {
-        e = launch_mfma<4, 4, 2, 2>(x, w_packed, w_scales, out, m, n, k, plan.splits, t, rank ? lb : nullptr,
-                                    rank, lora_scale, stream);
+        e = launch_mfma<4, 4, 2, 2, kWidePD>(x, w_packed, w_scales, out, m, n, k, plan.splits, tpart, plan.t_splits,
+                                             lbp, rank, lora_scale, stream);
     }
     if (e != hipSuccess || plan.splits == 1) return e;
     const size_t count = static_cast<size_t>(m) * n;
