@@ -20,6 +20,48 @@ __device__ __forceinline__ float nibble_signed(uint32_t w, int t) {
     return static_cast<float>(static_cast<int32_t>(w << (28 - 4 * t)) >> 28);
 }
 
+// v_cvt_off_f32_i4 reads bits 3..0 of its operand as a two's-complement value v
+// and returns v / 16 exactly. The SDWA forms read byte 1, 2 or 3 of the operand
+// in place, so a byte's low nibble needs no shift.
+#define SPACESLUG_CVT_OFF_BYTE(SEL)                                                                      \
+    __device__ __forceinline__ float cvt_off_##SEL(uint32_t w) {                                          \
+        float r;                                                                                         \
+        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:" #SEL : "=v"(r) \
+            : "v"(w));                                                                                   \
+        return r;                                                                                        \
+    }
+SPACESLUG_CVT_OFF_BYTE(BYTE_1)
+SPACESLUG_CVT_OFF_BYTE(BYTE_2)
+SPACESLUG_CVT_OFF_BYTE(BYTE_3)
+#undef SPACESLUG_CVT_OFF_BYTE
+
+// Signed decode of all 8 nibbles of w: f[t] = v_t / 16 exactly, in 9 VALU ops
+// (one shift for the odd nibbles, eight conversions). A sum of x * f times 16
+// (exact) is the sum of x * v.
+__device__ __forceinline__ void nibbles_signed_16th(uint32_t w, float (&f)[8]) {
+    const uint32_t wo = w >> 4;
+    f[0] = __builtin_amdgcn_cvt_off_f32_i4(static_cast<int>(w));
+    f[1] = __builtin_amdgcn_cvt_off_f32_i4(static_cast<int>(wo));
+    f[2] = cvt_off_BYTE_1(w);
+    f[3] = cvt_off_BYTE_1(wo);
+    f[4] = cvt_off_BYTE_2(w);
+    f[5] = cvt_off_BYTE_2(wo);
+    f[6] = cvt_off_BYTE_3(w);
+    f[7] = cvt_off_BYTE_3(wo);
+}
+
+// The same values with compiler-visible instructions only (shifts plus the
+// conversion builtin, about 13 VALU ops). Use this one where the results feed
+// MFMA operands: the hazard recognizer does not see inside inline asm, and an
+// asm write to a VGPR that an in-flight MFMA still reads as SrcB corrupts it.
+__device__ __forceinline__ void nibbles_signed_16th_mfma(uint32_t w, float (&f)[8]) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) f[t] = __builtin_amdgcn_cvt_off_f32_i4(static_cast<int>(w >> (4 * t)));
+}
+
+// Scale that restores nibbles_signed_16th's values to the integers v.
+constexpr float kSixteenthsUnit = 16.0f;
+
 // Offset-binary decode of all 8 nibbles of w through the fp8 converter.
 // u = v + 8 = nibble ^ 8 lies in [0, 15]; a byte holding u read as OCP e4m3
 // (bias 7) is exactly u * 2^-9 (u < 8 is a subnormal m/8 * 2^-6, u >= 8 has

@@ -7,8 +7,9 @@
 //     q with k = 8q + t at step t = 0..7, so its B operands for column j are
 //     the 8 nibbles of ONE 32-bit word of the packed column (word q of the
 //     group's 16 bytes) and its A operands are 8 consecutive floats of row j
-//     (two 128-bit loads). Weights are decoded in registers (v_bfe_i32 +
-//     v_cvt_f32_i32, exact small integers) straight into the MFMA operand;
+//     (two 128-bit loads). Weights are decoded in registers to v / 16
+//     (v_cvt_off_f32_i4, exact; the factor 16 joins the scale) straight into
+//     the MFMA operand;
 //   - the MFMA accumulates P = x * v over one group (8 steps) in fp32 from
 //     zero, and the group is folded into a float64 accumulator as
 //     acc += (double)s * P. Scale application moves out of the inner loop, and
@@ -127,22 +128,22 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void q4_gemm_mfma_kernel(
     // One group: P = x * v over 32 K values on the MFMA from zero, then acc += s * P.
     auto do_group = [&](const GroupOps<WM, WN>& o) {
         f32x4 P[WM][WN];
+        float bv[WN][8];
+#pragma unroll
+        for (int tn = 0; tn < WN; ++tn) nibbles_signed_16th_mfma(o.bw[tn], bv[tn]);
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            float bv[WN];
-#pragma unroll
-            for (int tn = 0; tn < WN; ++tn) bv[tn] = nibble_signed(o.bw[tn], t);
 #pragma unroll
             for (int tm = 0; tm < WM; ++tm) {
                 const float av = t < 4 ? o.alo[tm][t & 3] : o.ahi[tm][t & 3];
 #pragma unroll
                 for (int tn = 0; tn < WN; ++tn)
-                    P[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[tn], t == 0 ? zero : P[tm][tn], 0, 0, 0);
+                    P[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[tn][t], t == 0 ? zero : P[tm][tn], 0, 0, 0);
             }
         }
 #pragma unroll
         for (int tn = 0; tn < WN; ++tn) {
-            const double sc = static_cast<double>(o.bs[tn]);
+            const double sc = static_cast<double>(o.bs[tn]) * kSixteenthsUnit;
 #pragma unroll
             for (int tm = 0; tm < WM; ++tm)
 #pragma unroll
@@ -183,23 +184,23 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void q4_gemm_mfma_kernel(
                     bs_n[tn] = scol[tn][gn];
                 }
                 f32x4 P[WM][WN];
+                float bv[WN][8];
+#pragma unroll
+                for (int tn = 0; tn < WN; ++tn) nibbles_signed_16th_mfma(bw[tn], bv[tn]);
 #pragma unroll
                 for (int t = 0; t < 8; ++t) {
-                    float bv[WN];
-#pragma unroll
-                    for (int tn = 0; tn < WN; ++tn) bv[tn] = nibble_signed(bw[tn], t);
 #pragma unroll
                     for (int tm = 0; tm < WM; ++tm) {
                         const float av = t < 4 ? alo[tm][t & 3] : ahi[tm][t & 3];
 #pragma unroll
                         for (int tn = 0; tn < WN; ++tn)
-                            P[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[tn], t == 0 ? zero : P[tm][tn], 0,
-                                                                             0, 0);
+                            P[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[tn][t], t == 0 ? zero : P[tm][tn],
+                                                                             0, 0, 0);
                     }
                 }
 #pragma unroll
                 for (int tn = 0; tn < WN; ++tn) {
-                    const double sc = static_cast<double>(bs[tn]);
+                    const double sc = static_cast<double>(bs[tn]) * kSixteenthsUnit;
 #pragma unroll
                     for (int tm = 0; tm < WM; ++tm)
 #pragma unroll

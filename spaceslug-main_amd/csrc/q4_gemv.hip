@@ -13,14 +13,12 @@
 //     issued before any arithmetic, so the whole wavefront's data is in flight
 //     at once; the columns are then consumed in issue order as they land;
 //   - x stays in registers for the whole chunk (the lane's own groups), read
-//     straight from global memory (it is tiny and L1/L2 resident), together
-//     with each group's pairwise sum of x divided by 64;
-//   - nibbles are decoded in registers to (v + 8) * 2^-9 by v_cvt_pk_f32_fp8
-//     (nibbles_offset_e4m3), so a group partial is
-//     sum x (v + 8) 2^-9 - sum x / 64 = 2^-9 * sum x v; it is scaled by s and
-//     accumulated per lane; the 64 lane partials of a column are summed with
-//     DPP row operations plus two row broadcasts, and the 2^9 factor restored
-//     exactly at the end.
+//     straight from global memory (it is tiny and L1/L2 resident);
+//   - nibbles are decoded in registers to v / 16 by v_cvt_off_f32_i4
+//     (nibbles_signed_16th, exact), so a group partial is 2^-4 * sum x v with
+//     no offset to cancel; it is scaled by s and accumulated per lane; the 64
+//     lane partials of a column are summed with DPP row operations plus two
+//     row broadcasts, and the factor 16 restored exactly at the end.
 // K larger than one chunk (64 * SPC groups per lane pass) is walked in chunks.
 #include "q4_device.hpp"
 #include "q4_kernels.hpp"
@@ -44,18 +42,6 @@ __device__ __forceinline__ float wave_reduce_dpp(float v) {
     v += dpp_src<0x142, 0xA>(v);   // row_bcast:15 into rows 1 and 3
     v += dpp_src<0x143, 0xC>(v);   // row_bcast:31 into rows 2 and 3 -> row 3 holds the total
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-
-// Pairwise sum of 32 floats (error grows with log2(32), not 32).
-__device__ __forceinline__ float pairwise32(const float (&v)[32]) {
-    float t[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) t[i] = v[2 * i] + v[2 * i + 1];
-#pragma unroll
-    for (int w = 8; w >= 1; w >>= 1)
-#pragma unroll
-        for (int i = 0; i < w; ++i) t[i] = t[2 * i] + t[2 * i + 1];
-    return t[0];
 }
 
 // Loads of one K chunk for CPW columns: x first (coalesced, into xr), then every
@@ -128,7 +114,6 @@ __device__ __forceinline__ void consume_chunk(ChunkLoads<M, SPC, CPW>& L, f32x4*
         }
     __syncthreads();
     float xv[M][SPC][32];
-    float cr[M][SPC];
 #pragma unroll
     for (int m = 0; m < M; ++m) {
 #pragma unroll
@@ -142,7 +127,6 @@ __device__ __forceinline__ void consume_chunk(ChunkLoads<M, SPC, CPW>& L, f32x4*
                 xv[m][s][4 * q + 2] = t[2];
                 xv[m][s][4 * q + 3] = t[3];
             }
-            cr[m][s] = pairwise32(xv[m][s]) * (1.0f / 64.0f);
         }
     }
     // Groups past K contribute through a zero scale: a select, not a branch, so no
@@ -159,7 +143,7 @@ __device__ __forceinline__ void consume_chunk(ChunkLoads<M, SPC, CPW>& L, f32x4*
         for (int s = 0; s < SPC; ++s) {
             float f[32];
 #pragma unroll
-            for (int w = 0; w < 4; ++w) nibbles_offset_e4m3(L.wv[c][s][w], *reinterpret_cast<float(*)[8]>(&f[8 * w]));
+            for (int w = 0; w < 4; ++w) nibbles_signed_16th(L.wv[c][s][w], *reinterpret_cast<float(*)[8]>(&f[8 * w]));
 #pragma unroll
             for (int m = 0; m < M; ++m) {
                 float p0 = 0.0f, p1 = 0.0f;
@@ -168,8 +152,7 @@ __device__ __forceinline__ void consume_chunk(ChunkLoads<M, SPC, CPW>& L, f32x4*
                     p0 = fmaf(xv[m][s][k], f[k], p0);
                     p1 = fmaf(xv[m][s][16 + k], f[16 + k], p1);
                 }
-                const float d = (p0 + p1) - cr[m][s];
-                acc[c][m] = fmaf(L.sc[c][s], d, acc[c][m]);
+                acc[c][m] = fmaf(L.sc[c][s], p0 + p1, acc[c][m]);
             }
         }
     }
@@ -217,7 +200,7 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const float* x,  
 #pragma unroll
         for (int m = 0; m < M; ++m) {
             const float total = wave_reduce_dpp(acc[c][m]);
-            if (lane == 0 && col < N) y[static_cast<size_t>(m) * N + col] = total * kE4m3OffsetUnit;
+            if (lane == 0 && col < N) y[static_cast<size_t>(m) * N + col] = total * kSixteenthsUnit;
         }
     }
 }
@@ -250,13 +233,13 @@ __device__ __forceinline__ void pipe_issue(PipeSlot<SPC, D>& slot, const u32x4* 
 
 template <int SPC, int D>
 __device__ __forceinline__ float pipe_column(const PipeSlot<SPC, D>& slot, const float (&xv)[SPC][32],
-                                             const float (&cr)[SPC], const bool (&valid)[SPC]) {
+                                             const bool (&valid)[SPC]) {
     float acc = 0.0f;
 #pragma unroll
     for (int s = 0; s < SPC; ++s) {
         float f[32];
 #pragma unroll
-        for (int w = 0; w < 4; ++w) nibbles_offset_e4m3(slot.wv[s][w], *reinterpret_cast<float(*)[8]>(&f[8 * w]));
+        for (int w = 0; w < 4; ++w) nibbles_signed_16th(slot.wv[s][w], *reinterpret_cast<float(*)[8]>(&f[8 * w]));
         float p0 = 0.0f, p1 = 0.0f;
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
@@ -264,7 +247,7 @@ __device__ __forceinline__ float pipe_column(const PipeSlot<SPC, D>& slot, const
             p1 = fmaf(xv[s][16 + k], f[16 + k], p1);
         }
         const float sc = valid[s] ? slot.sc[s] : 0.0f;
-        acc = fmaf(sc, (p0 + p1) - cr[s], acc);
+        acc = fmaf(sc, p0 + p1, acc);
     }
     return wave_reduce_dpp(acc);
 }
@@ -321,7 +304,6 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
     }
     __syncthreads();
     float xv[SPC][32];
-    float cr[SPC];
 #pragma unroll
     for (int s = 0; s < SPC; ++s) {
         const int gl = 64 * s + lane;
@@ -333,7 +315,6 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
             xv[s][4 * q + 2] = t[2];
             xv[s][4 * q + 3] = t[3];
         }
-        cr[s] = pairwise32(xv[s]) * (1.0f / 64.0f);
     }
 
     // Steady state: compute slot d (column i), then refill it with column i + D.
@@ -342,7 +323,7 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
     for (int it = 0; it + 1 < iters; ++it) {
 #pragma unroll
         for (int d = 0; d < D; ++d, ++i) {
-            const float t = pipe_column<SPC, D>(slot[d], xv, cr, valid);
+            const float t = pipe_column<SPC, D>(slot[d], xv, valid);
             result = lane == i ? t : result;
             pipe_issue<SPC, D>(slot[d], wq, ws, col0 + i + D, N, G, off16, off4);
             // Keep the next slot's arithmetic below this refill: otherwise the scheduler
@@ -352,11 +333,11 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
     }
 #pragma unroll
     for (int d = 0; d < D; ++d, ++i) {
-        const float t = pipe_column<SPC, D>(slot[d], xv, cr, valid);
+        const float t = pipe_column<SPC, D>(slot[d], xv, valid);
         result = lane == i ? t : result;
     }
     // lane c holds column col0 + c: one coalesced store of the wavefront's run
-    if (lane < cpb && col0 + lane < N) y[col0 + lane] = result * kE4m3OffsetUnit;
+    if (lane < cpb && col0 + lane < N) y[col0 + lane] = result * kSixteenthsUnit;
 }
 
 template <int M, int SPC, int CPW>
