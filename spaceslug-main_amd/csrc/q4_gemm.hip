@@ -23,9 +23,13 @@
 //     rows and weight columns within its L2;
 //   - when the grid is too small to fill 256 CUs, K is split across
 //     blockIdx.y and a second kernel sums the partials in a fixed order.
-// LoRA: lora_t_kernel computes T = x * la on the MFMA as K-split partials; the
-// GEMM epilogue sums them and adds scale * T[rows] * lb[:, cols] with the same
-// MFMA tile layout (r in the K slot), before the single store of y.
+// LoRA: lora_t_kernel computes T = x * la on the MFMA as K-split partials,
+// split_reduce_kernel sums them once into T (M x R), and the GEMM epilogue adds
+// scale * T[rows] * lb[:, cols] with the same MFMA tile layout (r in the K
+// slot) before the single store of y (summing the partials in every tile's
+// epilogue instead cost 70 us of 280 at M=512, K=N=4096, r=16).
+#include <algorithm>
+
 #include "q4_device.hpp"
 #include "q4_kernels.hpp"
 
@@ -83,8 +87,9 @@ template <int WM, int WN, int WAVES_M, int WAVES_N, int PD>
 // the compiler would be free to re-issue the prefetched group's loads at their
 // use (to save registers), which serialises them behind the compute.
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void q4_gemm_mfma_kernel(
-    const float* x, const uint32_t* wq, const float* ws, float* __restrict__ out, int M, int N, int K, int tiles_m, int tiles_n, int groups_per_split,
-    const float* __restrict__ tpart, int t_splits, const float* __restrict__ lb, int R, float lscale) {
+    const float* x, const uint32_t* wq, const float* ws, float* __restrict__ out, int M, int N, int K, int tiles_m,
+    int tiles_n, int groups_per_split, const float* __restrict__ tmat, const float* __restrict__ lb, int R,
+    float lscale) {
     using Shape = TileShape<WM, WN, WAVES_M, WAVES_N>;
     const int lane = threadIdx.x & 63;
     const int wid = threadIdx.x >> 6;
@@ -246,8 +251,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void q4_gemm_mfma_kernel(
     }
 
     if (lb != nullptr && blockIdx.y == 0) {
-        // LoRA epilogue: + lscale * T[m0.., :R] * lb[:R, n0..] on the MFMA, r in the K slot,
-        // with T = sum over the t_splits partials of lora_t_kernel.
+        // LoRA epilogue: + lscale * T[m0.., :R] * lb[:R, n0..] on the MFMA, r in the K slot
+        // (T = x * la, M x R, summed by lora_t_reduce_kernel).
 #pragma unroll
         for (int tm = 0; tm < WM; ++tm) {
             const int row = min(m0 + 16 * tm + j, M - 1);
@@ -257,11 +262,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void q4_gemm_mfma_kernel(
                 f32x4 P = zero;
                 for (int r0 = 0; r0 < R; r0 += 4) {
                     const int r = r0 + q;
-                    float av = 0.0f;
-                    if (r < R) {
-                        for (int s = 0; s < t_splits; ++s)
-                            av += tpart[(static_cast<size_t>(s) * M + row) * R + r];
-                    }
+                    const float av = r < R ? tmat[static_cast<size_t>(row) * R + r] : 0.0f;
                     const float bv = r < R ? lb[static_cast<size_t>(r) * N + col] : 0.0f;
                     P = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, P, 0, 0, 0);
                 }
@@ -338,7 +339,8 @@ __global__ __launch_bounds__(64) void lora_t_kernel(const float* __restrict__ x,
     }
 }
 
-// y[i] = sum_s part[s][i], in ascending s, accumulated in double.
+// y[i] = sum_s part[s][i], in ascending s, accumulated in double (K-split
+// partials of the GEMM, and of the LoRA pre-pass T = x * la).
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ part,
                                                            float* __restrict__ y, size_t count,
                                                            int splits) {
@@ -352,8 +354,8 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
 
 template <int WM, int WN, int WAVES_M, int WAVES_N, int PD>
 hipError_t launch_mfma(const float* x, const uint8_t* w_packed, const float* w_scales, float* out,
-                       uint32_t m, uint32_t n, uint32_t k, int splits, const float* tpart, int t_splits,
-                       const float* lb, uint32_t rank, float lscale, hipStream_t stream) {
+                       uint32_t m, uint32_t n, uint32_t k, int splits, const float* tmat, const float* lb,
+                       uint32_t rank, float lscale, hipStream_t stream) {
     using Shape = TileShape<WM, WN, WAVES_M, WAVES_N>;
     const int tiles_m = static_cast<int>((m + Shape::kBM - 1) / Shape::kBM);
     const int tiles_n = static_cast<int>((n + Shape::kBN - 1) / Shape::kBN);
@@ -363,16 +365,20 @@ hipError_t launch_mfma(const float* x, const uint8_t* w_packed, const float* w_s
                        dim3(tiles_m * tiles_n, splits), dim3(Shape::kThreads), 0, stream, x,
                        reinterpret_cast<const uint32_t*>(w_packed), w_scales, out,
                        static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), tiles_m,
-                       tiles_n, gps, tpart, t_splits, lb, static_cast<int>(rank), lscale);
+                       tiles_n, gps, tmat, lb, static_cast<int>(rank), lscale);
     return hipGetLastError();
 }
 
 // Tile shapes: skinny = one 16-row MFMA tile x 256 columns per workgroup
-// (4 waves of 16 x 64), 4 groups in flight; wide = 128 x 128 per workgroup
-// (2 x 2 waves of 64 x 64), 1 group in flight (register bound: 128 double
-// accumulators + 64 MFMA accumulators per lane).
+// (4 waves of 16 x 64), 2 groups in flight (M=16, K=N=4096: 19.0 us per call
+// against 22.3 us with 4); wide = 128 x 128 per workgroup (2 x 2 waves of
+// 64 x 64), 1 group in flight (register bound: 64 double accumulators + 64
+// MFMA accumulators per lane). Measured slower at M=2048: 64 x 32 wave tiles
+// at two waves per SIMD, a second MFMA accumulator set, and the flush split
+// in halves interleaved with the MFMAs (VALU instructions cost matrix-core
+// issue cycles whether interleaved or not).
 using SkinnyShape = TileShape<1, 4, 1, 4>;
-constexpr int kSkinnyPD = 4;
+constexpr int kSkinnyPD = 2;
 using WideShape = TileShape<4, 4, 2, 2>;
 constexpr int kWidePD = 1;
 
@@ -399,7 +405,9 @@ Q4Plan plan_q4gemm(const DeviceInfo& dev, uint32_t m, uint32_t n, uint32_t k, ui
     }
     const size_t tiles = static_cast<size_t>((m + bm - 1) / bm) * ((n + bn - 1) / bn);
     const size_t waves = tiles * waves_per_tile;
-    const size_t target = static_cast<size_t>(8) * dev.cu_count;  // two waves per SIMD
+    // Resident wavefronts per SIMD at these register counts: skinny 3 (2 targeted), wide 1.
+    const size_t waves_per_simd = plan.kind == Q4Plan::kMfmaSkinny ? 2 : 1;
+    const size_t target = 4 * waves_per_simd * static_cast<size_t>(dev.cu_count);
     const int groups = static_cast<int>(k / kGroup);
     const int min_groups = plan.kind == Q4Plan::kMfmaSkinny ? 8 : 4;
     int splits = 1;
@@ -412,7 +420,8 @@ Q4Plan plan_q4gemm(const DeviceInfo& dev, uint32_t m, uint32_t n, uint32_t k, ui
     if (splits > 1) bytes += align_up(static_cast<size_t>(splits) * m * n * sizeof(float));
     if (rank > 0) {
         plan.t_splits = (groups + kLoraGroupsPerWave - 1) / kLoraGroupsPerWave;
-        bytes += align_up(static_cast<size_t>(plan.t_splits) * m * rank * sizeof(float));
+        bytes += align_up(static_cast<size_t>(plan.t_splits) * m * rank * sizeof(float));  // T partials
+        bytes += align_up(static_cast<size_t>(m) * rank * sizeof(float));                  // T
     }
     plan.workspace_bytes = bytes;
     return plan;
@@ -430,23 +439,31 @@ hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float*
         partial = reinterpret_cast<float*>(wsp);
         wsp += align_up(static_cast<size_t>(plan.splits) * m * n * sizeof(float));
     }
-    float* tpart = nullptr;
+    float* tmat = nullptr;
     if (rank > 0) {
-        tpart = reinterpret_cast<float*>(wsp);
+        float* tpart = reinterpret_cast<float*>(wsp);
+        wsp += align_up(static_cast<size_t>(plan.t_splits) * m * rank * sizeof(float));
+        tmat = reinterpret_cast<float*>(wsp);
         hipLaunchKernelGGL(lora_t_kernel, dim3((m + 15) / 16, (rank + 15) / 16, plan.t_splits), dim3(64), 0, stream,
                            x, la, tpart, static_cast<int>(m), static_cast<int>(k), static_cast<int>(rank));
         hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const size_t tcount = static_cast<size_t>(m) * rank;
+        const size_t tblocks = std::min((tcount + 255) / 256, static_cast<size_t>(dev.cu_count) * 8);
+        hipLaunchKernelGGL(split_reduce_kernel, dim3(static_cast<unsigned>(tblocks)), dim3(256), 0, stream, tpart,
+                           tmat, tcount, plan.t_splits);
+        e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
     float* out = plan.splits > 1 ? partial : y;
     const float* lbp = rank ? lb : nullptr;
     hipError_t e;
     if (plan.kind == Q4Plan::kMfmaSkinny) {
-        e = launch_mfma<1, 4, 1, 4, kSkinnyPD>(x, w_packed, w_scales, out, m, n, k, plan.splits, tpart, plan.t_splits,
-                                               lbp, rank, lora_scale, stream);
+        e = launch_mfma<1, 4, 1, 4, kSkinnyPD>(x, w_packed, w_scales, out, m, n, k, plan.splits, tmat, lbp, rank,
+                                               lora_scale, stream);
     } else {
-        e = launch_mfma<4, 4, 2, 2, kWidePD>(x, w_packed, w_scales, out, m, n, k, plan.splits, tpart, plan.t_splits,
-                                             lbp, rank, lora_scale, stream);
+        e = launch_mfma<4, 4, 2, 2, kWidePD>(x, w_packed, w_scales, out, m, n, k, plan.splits, tmat, lbp, rank,
+                                             lora_scale, stream);
     }
     if (e != hipSuccess || plan.splits == 1) return e;
     const size_t count = static_cast<size_t>(m) * n;

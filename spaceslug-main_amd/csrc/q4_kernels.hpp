@@ -20,7 +20,7 @@ constexpr int kGemvMaxRows = 4;
 struct Q4Plan {
     enum Kind { kGemv, kMfmaSkinny, kMfmaWide } kind;
     int splits;              // K-splits of the MFMA kernel (1 = write y directly)
-    size_t workspace_bytes;  // device scratch the call needs (split partials + LoRA T partials)
+    size_t workspace_bytes;  // device scratch the call needs (split partials, LoRA T partials and T)
     int t_splits;            // K-splits of the LoRA pre-pass T = x * lora_a (0 without LoRA)
 };
 
