@@ -96,8 +96,10 @@ int spaceslug_q4gemm_lora(const float* x, const uint8_t* w_packed, const float* 
  * arguments; the MFMA path, when it splits K across workgroups, keeps its
  * partial sums in a library-owned device workspace that is allocated on first
  * use and grown on demand (growth synchronises the device, steady state does
- * not allocate). Calls that share a device share that workspace, so they must
- * not overlap (same single-threaded rule as above). */
+ * not allocate). Calls that share a device share that workspace; the library
+ * orders them: a call on a stream other than the previous user's makes its
+ * stream wait (on the GPU, hipStreamWaitEvent) for that user's kernels, and
+ * host threads are serialised while enqueueing. */
 int spaceslug_q4gemm_device(const float* d_x, const uint8_t* d_w_packed, const float* d_w_scales,
                             float* d_y, uint32_t m, uint32_t n, uint32_t k, void* stream);
 

@@ -347,7 +347,16 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
     const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
     for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += stride) {
         double s = 0.0;
-        for (int z = 0; z < splits; ++z) s += static_cast<double>(part[static_cast<size_t>(z) * count + i]);
+        int z = 0;
+        // eight loads in flight per thread, summed in ascending z
+        for (; z + 8 <= splits; z += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = part[static_cast<size_t>(z + u) * count + i];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s += static_cast<double>(v[u]);
+        }
+        for (; z < splits; ++z) s += static_cast<double>(part[static_cast<size_t>(z) * count + i]);
         y[i] = static_cast<float>(s);
     }
 }

@@ -50,12 +50,16 @@ int from_hip(const HipError& e) {
 }
 
 // Per-device state: launch-relevant properties and the grow-only workspace of
-// the device-pointer entry points.
+// the device-pointer entry points. ws_done marks the end of the last call that
+// used the workspace, on ws_stream; a call on another stream waits for it.
 struct DeviceState {
     bool ready = false;
     spaceslug::DeviceInfo info{};
     void* workspace = nullptr;
     size_t workspace_bytes = 0;
+    hipEvent_t ws_done = nullptr;
+    hipStream_t ws_stream = nullptr;
+    bool ws_used = false;
 };
 
 std::mutex g_device_mutex;
@@ -90,11 +94,11 @@ DeviceState& current_device() {
     return d;
 }
 
-// Returns the device workspace holding at least `bytes`; growing it waits for
-// the device so no queued kernel still reads the old buffer.
+// Returns the device workspace holding at least `bytes` (the caller holds
+// g_device_mutex); growing it waits for the device so no queued kernel still
+// reads the old buffer.
 void* device_workspace(DeviceState& d, size_t bytes) {
     if (bytes == 0) return nullptr;
-    std::lock_guard<std::mutex> lock(g_device_mutex);
     if (d.workspace_bytes < bytes) {
         if (d.workspace) {
             check(hipDeviceSynchronize(), "hipDeviceSynchronize (workspace growth)");
@@ -191,10 +195,24 @@ int run_device(const float* dx, const uint8_t* dw, const float* ds, const float*
                void* stream) {
     DeviceState& dev = current_device();
     const spaceslug::Q4Plan plan = spaceslug::plan_q4gemm(dev.info, m, n, k, rank);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (plan.workspace_bytes == 0) {
+        check(spaceslug::launch_q4gemm(plan, dev.info, dx, dw, ds, dy, m, n, k, dla, dlb, rank, lora_scale, nullptr,
+                                       st),
+              "q4gemm launch");
+        return ok();
+    }
+    // Calls that use the shared workspace are ordered across streams: a call on a
+    // stream other than the previous user's waits (on the GPU) for that user's end.
+    std::lock_guard<std::mutex> lock(g_device_mutex);
     void* dws = device_workspace(dev, plan.workspace_bytes);
-    check(spaceslug::launch_q4gemm(plan, dev.info, dx, dw, ds, dy, m, n, k, dla, dlb, rank, lora_scale, dws,
-                                   static_cast<hipStream_t>(stream)),
+    if (!dev.ws_done) check(hipEventCreateWithFlags(&dev.ws_done, hipEventDisableTiming), "hipEventCreateWithFlags");
+    if (dev.ws_used && dev.ws_stream != st) check(hipStreamWaitEvent(st, dev.ws_done, 0), "hipStreamWaitEvent");
+    check(spaceslug::launch_q4gemm(plan, dev.info, dx, dw, ds, dy, m, n, k, dla, dlb, rank, lora_scale, dws, st),
           "q4gemm launch");
+    check(hipEventRecord(dev.ws_done, st), "hipEventRecord");
+    dev.ws_stream = st;
+    dev.ws_used = true;
     return ok();
 }
 

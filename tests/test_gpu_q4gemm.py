@@ -273,3 +273,26 @@ def test_device_entry_on_side_stream(session, oracle, gpu):
         x_t, w_t, s_t = to_dev(c.x, torch), to_dev(c.packed, torch), to_dev(c.scales, torch)
     y = run_device(session, torch, x_t, w_t, s_t, m, n, k, stream=s)
     check(oracle, y.cpu().numpy(), oracle.q4gemm_packed(c.x, c.packed, c.scales), label="side stream")
+
+
+def test_split_k_calls_on_two_streams(session, oracle, gpu):
+    """Two K-split calls (they share the library's device workspace) enqueued back to back on two
+    streams, several rounds: the second stream must wait for the first's partial sums to be consumed."""
+    import torch
+
+    m, n, k = 16, 2048, 4096
+    note("split-K workspace shared by two streams")
+    cases = [make_case(m, n, k, seed_a=0x100 + i, seed_b=0x200 + i, seed_s=0x300 + i) for i in range(2)]
+    want = [oracle.q4gemm_packed(c.x, c.packed, c.scales, threads=threads()) for c in cases]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    dev = [(to_dev(c.x, torch), to_dev(c.packed, torch), to_dev(c.scales, torch)) for c in cases]
+    torch.cuda.synchronize()
+    ys = [torch.empty((m, n), dtype=torch.float32, device="cuda:0") for _ in range(2)]
+    for _ in range(4):
+        for i in range(2):
+            x_t, w_t, s_t = dev[i]
+            session.q4gemm_device(x_t.data_ptr(), w_t.data_ptr(), s_t.data_ptr(), ys[i].data_ptr(), m, n, k,
+                                  streams[i].cuda_stream)
+    torch.cuda.synchronize()
+    for i in range(2):
+        check(oracle, ys[i].cpu().numpy(), want[i], label=f"stream {i}")
