@@ -57,4 +57,27 @@ __device__ __forceinline__ void nibbles_signed_16th_mfma(uint32_t w, float (&f)[
 // Scale that restores nibbles_signed_16th's values to the integers v.
 constexpr float kSixteenthsUnit = 16.0f;
 
+// The four 16-lane rows of a wavefront as a 4 x 4 transpose of 32-bit values:
+// on return, register c of row q holds what register q of row c held.
+// v_permlane32_swap exchanges rows 2-3 of its first operand with rows 0-1 of
+// its second, v_permlane16_swap the odd rows of the first with the even rows
+// of the second.
+__device__ __forceinline__ u32x4 transpose_rows(u32x4 r) {
+    const auto p02 = __builtin_amdgcn_permlane32_swap(r.x, r.z, false, false);
+    const auto p13 = __builtin_amdgcn_permlane32_swap(r.y, r.w, false, false);
+    const auto p01 = __builtin_amdgcn_permlane16_swap(p02[0], p13[0], false, false);
+    const auto p23 = __builtin_amdgcn_permlane16_swap(p02[1], p13[1], false, false);
+    return u32x4{p01[0], p01[1], p23[0], p23[1]};
+}
+
+// Row q holds s_q (one value per 16-lane row, per column lane); on return every
+// row holds {s_0, s_1, s_2, s_3}.
+__device__ __forceinline__ f32x4 gather_rows(float s) {
+    const uint32_t u = __float_as_uint(s);
+    const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    const auto b = __builtin_amdgcn_permlane16_swap(a[0], a[0], false, false);
+    const auto c = __builtin_amdgcn_permlane16_swap(a[1], a[1], false, false);
+    return f32x4{__uint_as_float(b[0]), __uint_as_float(b[1]), __uint_as_float(c[0]), __uint_as_float(c[1])};
+}
+
 }  // namespace spaceslug

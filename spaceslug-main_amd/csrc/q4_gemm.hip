@@ -1,4 +1,6 @@
 // fp32-MFMA int4 GEMM for 5+ rows (prefill, small-batch decode, LoRA projections).
+// Two kernels: q4_gemm_skinny_kernel for M <= 32 with K % 128 == 0 (described
+// at its definition) and q4_gemm_mfma_kernel for everything else, described here.
 //
 // Replaces q4gemm.comp:61-175 (64x64 tile, LDS-staged dequantised B, 4x4 FMA
 // micro-tile per thread) with a CDNA4 design built on v_mfma_f32_16x16x4_f32:
@@ -339,6 +341,114 @@ __global__ __launch_bounds__(64) void lora_t_kernel(const float* __restrict__ x,
     }
 }
 
+// Small-M GEMM (M <= 32, K % 128 == 0) with no K-split partials in memory: a
+// workgroup owns one 16 x 16 output tile and its KW wavefronts split K between
+// them; their float64 accumulators are summed through LDS in wavefront order
+// (deterministic), and the LoRA term, if any, is added in double before the
+// single store. Per wavefront, weights and scales move in units of 4 groups (a
+// "quad"): lane (j, q) loads column j's 16 bytes of group 4*quad + q (one
+// 128-bit load; the 4 lanes of a column read 64 contiguous bytes) and its
+// scale, then a 4 x 4 transpose across the 16-lane rows (v_permlane*_swap)
+// gives every lane word q of each of the 4 groups, the MFMA B layout. Two quads
+// are in flight while one computes (statically named buffers E and O).
+// Measured at M=16, K=N=4096: 16.4 us per call against 20.5 us for the split-K
+// kernel plus its reduction, and ~16 us for every other split tried.
+constexpr int kSkinnyWaves = 8;
+
+struct QuadOps {
+    f32x4 alo[4], ahi[4];  // x[row j][32 g + 8 q .. +7] for the quad's 4 groups
+    u32x4 bw;              // column j, group 4 * quad + q: its 16 packed bytes
+    float bs;              // scale of column j, group 4 * quad + q
+};
+
+__device__ __forceinline__ void load_quad(QuadOps& o, const float* arow, const u32x4* bq, const float* sq, int qi) {
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) {
+        o.alo[gi] = *reinterpret_cast<const f32x4*>(arow + (4 * qi + gi) * 32);
+        o.ahi[gi] = *reinterpret_cast<const f32x4*>(arow + (4 * qi + gi) * 32 + 4);
+    }
+    o.bw = __builtin_nontemporal_load(bq + 4 * qi);
+    o.bs = __builtin_nontemporal_load(sq + 4 * qi);
+}
+
+__device__ __forceinline__ void mma_quad(const QuadOps& o, double (&acc)[4]) {
+    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    const u32x4 bw = transpose_rows(o.bw);  // word q of each of the quad's groups
+    const f32x4 bs = gather_rows(o.bs);     // the quad's 4 scales of column j
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) {
+        float bv[8];
+        nibbles_signed_16th_mfma(bw[gi], bv);
+        f32x4 P;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const float av = t < 4 ? o.alo[gi][t & 3] : o.ahi[gi][t & 3];
+            P = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[t], t == 0 ? zero : P, 0, 0, 0);
+        }
+        const double sc = static_cast<double>(bs[gi]) * kSixteenthsUnit;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = fma(sc, static_cast<double>(P[r]), acc[r]);
+    }
+}
+
+template <int KW>
+// x, wq and ws are not __restrict__ for the reason given at q4_gemm_mfma_kernel.
+__global__ __launch_bounds__(64 * KW) void q4_gemm_skinny_kernel(const float* x, const uint32_t* wq, const float* ws,
+                                                                float* __restrict__ y, int M, int N, int K,
+                                                                int tiles_m, const float* __restrict__ tmat,
+                                                                const float* __restrict__ lb, int R, float lscale) {
+    const int lane = threadIdx.x & 63;
+    const int wk = threadIdx.x >> 6;
+    const int j = lane & 15;
+    const int q = lane >> 4;
+    const int G = K >> 5;
+    const int Q = G >> 2;
+    const int m0 = (blockIdx.x % tiles_m) * 16;
+    const int n0 = (blockIdx.x / tiles_m) * 16;
+    const int qpw = (Q + KW - 1) / KW;
+    const int qb = wk * qpw;
+    const int qe = min(Q, qb + qpw);
+    const int row = min(m0 + j, M - 1);
+    const int col = min(n0 + j, N - 1);
+    const float* arow = x + static_cast<size_t>(row) * K + 8 * q;
+    const u32x4* bq = reinterpret_cast<const u32x4*>(wq + static_cast<size_t>(col) * (K >> 3)) + q;
+    const float* sq = ws + static_cast<size_t>(col) * G + q;
+
+    double acc[4] = {0.0, 0.0, 0.0, 0.0};
+    if (qb < qe) {  // uniform per wavefront
+        QuadOps E, O;
+        load_quad(E, arow, bq, sq, qb);
+        load_quad(O, arow, bq, sq, min(qb + 1, qe - 1));
+        for (int qi = qb; qi < qe; qi += 2) {
+            mma_quad(E, acc);
+            load_quad(E, arow, bq, sq, min(qi + 2, qe - 1));  // past the end: a clamped reload, never used
+            if (qi + 1 < qe) mma_quad(O, acc);
+            load_quad(O, arow, bq, sq, min(qi + 3, qe - 1));
+        }
+    }
+
+    __shared__ double red[KW][256];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wk][(4 * q + r) * 16 + j] = acc[r];
+    __syncthreads();
+    for (int e = threadIdx.x; e < 256; e += 64 * KW) {
+        const int rr = m0 + (e >> 4);
+        const int cc = n0 + (e & 15);
+        if (rr >= M || cc >= N) continue;
+        double s = 0.0;
+#pragma unroll
+        for (int w = 0; w < KW; ++w) s += red[w][e];
+        if (lb != nullptr) {
+            double t = 0.0;
+            for (int r = 0; r < R; ++r)
+                t = fma(static_cast<double>(tmat[static_cast<size_t>(rr) * R + r]),
+                        static_cast<double>(lb[static_cast<size_t>(r) * N + cc]), t);
+            s = fma(static_cast<double>(lscale), t, s);
+        }
+        y[static_cast<size_t>(rr) * N + cc] = static_cast<float>(s);
+    }
+}
+
 // y[i] = sum_s part[s][i], in ascending s, accumulated in double (K-split
 // partials of the GEMM, and of the LoRA pre-pass T = x * la).
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ part,
@@ -378,9 +488,9 @@ hipError_t launch_mfma(const float* x, const uint8_t* w_packed, const float* w_s
     return hipGetLastError();
 }
 
-// Tile shapes: skinny = one 16-row MFMA tile x 256 columns per workgroup
-// (4 waves of 16 x 64), 2 groups in flight (M=16, K=N=4096: 19.0 us per call
-// against 22.3 us with 4); wide = 128 x 128 per workgroup (2 x 2 waves of
+// Tile shapes of q4_gemm_mfma_kernel: skinny split-K (M <= 32 with K not a
+// multiple of 128) = one 16-row MFMA tile x 256 columns per workgroup (4 waves
+// of 16 x 64), 2 groups in flight; wide = 128 x 128 per workgroup (2 x 2 waves of
 // 64 x 64), 1 group in flight (register bound: 64 double accumulators + 64
 // MFMA accumulators per lane). Measured slower at M=2048: 64 x 32 wave tiles
 // at two waves per SIMD, a second MFMA accumulator set, and the flush split
@@ -400,14 +510,26 @@ Q4Plan plan_q4gemm(const DeviceInfo& dev, uint32_t m, uint32_t n, uint32_t k, ui
     if (rank == 0 && m <= static_cast<uint32_t>(kGemvMaxRows)) {
         return plan;
     }
+    const int groups = static_cast<int>(k / kGroup);
+    size_t lora_bytes = 0;
+    if (rank > 0) {
+        plan.t_splits = (groups + kLoraGroupsPerWave - 1) / kLoraGroupsPerWave;
+        lora_bytes += align_up(static_cast<size_t>(plan.t_splits) * m * rank * sizeof(float));  // T partials
+        lora_bytes += align_up(static_cast<size_t>(m) * rank * sizeof(float));                  // T
+    }
+    if (m <= 32 && k % (4 * kGroup) == 0) {
+        plan.kind = Q4Plan::kSkinny;  // K split inside the workgroup: no partials in memory
+        plan.workspace_bytes = lora_bytes;
+        return plan;
+    }
     int bm, bn, waves_per_tile;
     if (m <= 32) {
-        plan.kind = Q4Plan::kMfmaSkinny;
+        plan.kind = Q4Plan::kSkinnySplitK;
         bm = SkinnyShape::kBM;
         bn = SkinnyShape::kBN;
         waves_per_tile = SkinnyShape::kWaves;
     } else {
-        plan.kind = Q4Plan::kMfmaWide;
+        plan.kind = Q4Plan::kWide;
         bm = WideShape::kBM;
         bn = WideShape::kBN;
         waves_per_tile = WideShape::kWaves;
@@ -415,23 +537,17 @@ Q4Plan plan_q4gemm(const DeviceInfo& dev, uint32_t m, uint32_t n, uint32_t k, ui
     const size_t tiles = static_cast<size_t>((m + bm - 1) / bm) * ((n + bn - 1) / bn);
     const size_t waves = tiles * waves_per_tile;
     // Resident wavefronts per SIMD at these register counts: skinny 3 (2 targeted), wide 1.
-    const size_t waves_per_simd = plan.kind == Q4Plan::kMfmaSkinny ? 2 : 1;
+    const size_t waves_per_simd = plan.kind == Q4Plan::kSkinnySplitK ? 2 : 1;
     const size_t target = 4 * waves_per_simd * static_cast<size_t>(dev.cu_count);
-    const int groups = static_cast<int>(k / kGroup);
-    const int min_groups = plan.kind == Q4Plan::kMfmaSkinny ? 8 : 4;
+    const int min_groups = plan.kind == Q4Plan::kSkinnySplitK ? 8 : 4;
     int splits = 1;
     while (waves * splits * 2 <= target && groups / (splits * 2) >= min_groups) splits *= 2;
     // Re-derive so that no split is empty.
     const int gps = (groups + splits - 1) / splits;
     splits = (groups + gps - 1) / gps;
     plan.splits = splits;
-    size_t bytes = 0;
+    size_t bytes = lora_bytes;
     if (splits > 1) bytes += align_up(static_cast<size_t>(splits) * m * n * sizeof(float));
-    if (rank > 0) {
-        plan.t_splits = (groups + kLoraGroupsPerWave - 1) / kLoraGroupsPerWave;
-        bytes += align_up(static_cast<size_t>(plan.t_splits) * m * rank * sizeof(float));  // T partials
-        bytes += align_up(static_cast<size_t>(m) * rank * sizeof(float));                  // T
-    }
     plan.workspace_bytes = bytes;
     return plan;
 }
@@ -467,7 +583,16 @@ hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float*
     float* out = plan.splits > 1 ? partial : y;
     const float* lbp = rank ? lb : nullptr;
     hipError_t e;
-    if (plan.kind == Q4Plan::kMfmaSkinny) {
+    if (plan.kind == Q4Plan::kSkinny) {
+        const int tiles_m = static_cast<int>((m + 15) / 16);
+        const int tiles_n = static_cast<int>((n + 15) / 16);
+        hipLaunchKernelGGL((q4_gemm_skinny_kernel<kSkinnyWaves>), dim3(tiles_m * tiles_n), dim3(64 * kSkinnyWaves),
+                           0, stream, x, reinterpret_cast<const uint32_t*>(w_packed), w_scales, y,
+                           static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), tiles_m, tmat, lbp,
+                           static_cast<int>(rank), lora_scale);
+        return hipGetLastError();
+    }
+    if (plan.kind == Q4Plan::kSkinnySplitK) {
         e = launch_mfma<1, 4, 1, 4, kSkinnyPD>(x, w_packed, w_scales, out, m, n, k, plan.splits, tmat, lbp, rank,
                                                lora_scale, stream);
     } else {

@@ -13,12 +13,14 @@ namespace spaceslug {
 // Scale group along K (q4gemm.comp:41,121): one fp32 scale per 32 K values.
 constexpr int kGroup = 32;
 
-// The decode GEMV handles 1..kGemvMaxRows rows; taller inputs go to the MFMA kernel.
+// The decode GEMV handles 1..kGemvMaxRows rows; taller inputs go to the MFMA kernels.
 constexpr int kGemvMaxRows = 4;
 
 // Launch shape chosen by plan_q4gemm for one call.
 struct Q4Plan {
-    enum Kind { kGemv, kMfmaSkinny, kMfmaWide } kind;
+    // kGemv: decode GEMV (m <= 4, no LoRA); kSkinny: m <= 32 with k % 128 == 0, K split
+    // inside the workgroup; kSkinnySplitK: other m <= 32; kWide: m > 32.
+    enum Kind { kGemv, kSkinny, kSkinnySplitK, kWide } kind;
     int splits;              // K-splits of the MFMA kernel (1 = write y directly)
     size_t workspace_bytes;  // device scratch the call needs (split partials, LoRA T partials and T)
     int t_splits;            // K-splits of the LoRA pre-pass T = x * lora_a (0 without LoRA)

@@ -85,6 +85,7 @@ def test_gemv_shapes(session, oracle, gpu, m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k", [(5, 1, 32), (5, 17, 96), (16, 256, 256), (17, 300, 1024), (32, 64, 64),
+                                   (16, 4096, 4064), (9, 40, 128), (31, 33, 384),
                                    (33, 129, 160), (100, 300, 512), (130, 260, 1056), (256, 512, 2048)])
 def test_mfma_shapes(session, oracle, gpu, m, n, k):
     note(f"mfma m={m} n={n} k={k}")
@@ -280,7 +281,7 @@ def test_split_k_calls_on_two_streams(session, oracle, gpu):
     streams, several rounds: the second stream must wait for the first's partial sums to be consumed."""
     import torch
 
-    m, n, k = 16, 2048, 4096
+    m, n, k = 64, 1024, 4096  # one row of 128x128 tiles: K is split 16 ways into the workspace
     note("split-K workspace shared by two streams")
     cases = [make_case(m, n, k, seed_a=0x100 + i, seed_b=0x200 + i, seed_s=0x300 + i) for i in range(2)]
     want = [oracle.q4gemm_packed(c.x, c.packed, c.scales, threads=threads()) for c in cases]
