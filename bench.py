@@ -55,10 +55,16 @@ def algo_flops(m: int, n: int, k: int, rank: int = 0) -> int:
     return f
 
 
-def make_weights(torch, n: int, k: int, copies: int, gen):
-    packed = [torch.randint(0, 256, (n, k // 2), dtype=torch.uint8, device="cuda", generator=gen) for _ in range(copies)]
-    scales = [torch.rand((n, k // 32), dtype=torch.float32, device="cuda", generator=gen) * 0.04 + 0.01
-              for _ in range(copies)]
+def make_weights(torch, n: int, k: int, copies: int, gen, with_all: bool = False):
+    """`copies` distinct weight matrices, stored back to back: copy i is rows [i*n, (i+1)*n) of one
+    [copies*n, k/2] packed tensor (and of one scale tensor), so the same bytes also form one matrix
+    of copies*n columns (the layout of concatenated projection weights)."""
+    packed_all = torch.randint(0, 256, (copies * n, k // 2), dtype=torch.uint8, device="cuda", generator=gen)
+    scales_all = torch.rand((copies * n, k // 32), dtype=torch.float32, device="cuda", generator=gen) * 0.04 + 0.01
+    packed = [packed_all[i * n:(i + 1) * n] for i in range(copies)]
+    scales = [scales_all[i * n:(i + 1) * n] for i in range(copies)]
+    if with_all:
+        return packed, scales, packed_all, scales_all
     return packed, scales
 
 
@@ -81,9 +87,10 @@ def time_region(torch, fn, steps: int, warmup: int) -> float:
 def bench_gemv(torch, session, steps: int, warmup: int, copies: int = 64, use_graph: bool = False) -> dict:
     m, n, k = 1, 14336, 4096
     gen = torch.Generator(device="cuda").manual_seed(1234)
-    packed, scales = make_weights(torch, n, k, copies, gen)
+    packed, scales, packed_all, scales_all = make_weights(torch, n, k, copies, gen, with_all=True)
     x = torch.randn((m, k), dtype=torch.float32, device="cuda", generator=gen)
     ys = [torch.empty((m, n), dtype=torch.float32, device="cuda") for _ in range(copies)]
+    y_all = torch.empty((m, copies * n), dtype=torch.float32, device="cuda")
 
     def sweep():
         st = torch.cuda.current_stream().cuda_stream
@@ -103,8 +110,20 @@ def bench_gemv(torch, session, steps: int, warmup: int, copies: int = 64, use_gr
     per_launch_s = ms * 1e-3 / copies
     bytes_per = algo_bytes(m, n, k)
     gbs = bytes_per / per_launch_s / 1e9
+
+    # The same 64 matrices read as one matrix of 64*n columns in a single launch: what the kernel
+    # streams when one launch's ramp-up and drain are amortised (fused projections sharing x).
+    def one_launch():
+        session.q4gemm_device(x.data_ptr(), packed_all.data_ptr(), scales_all.data_ptr(), y_all.data_ptr(), m,
+                              copies * n, k, torch.cuda.current_stream().cuda_stream)
+
+    ms_all = time_region(torch, one_launch, max(3, steps // 5), 2)
+    bytes_all = algo_bytes(m, copies * n, k)
+    concat = {"n": copies * n, "bytes": bytes_all, "us_per_launch": round(ms_all * 1e3, 3),
+              "gbs": round(bytes_all / (ms_all * 1e-3) / 1e9, 2),
+              "frac": round(bytes_all / (ms_all * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     return {"ms_per_step": ms, "per_launch_us": per_launch_s * 1e6, "gbs": gbs, "bytes_per_launch": bytes_per,
-            "copies": copies, "graph": use_graph,
+            "copies": copies, "graph": use_graph, "concatenated": concat,
             "tflops": algo_flops(m, n, k) / per_launch_s / 1e12}
 
 
@@ -258,6 +277,7 @@ def main() -> int:
                      "frac": round(gemv["gbs"] / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
                      "bytes_per_launch": gemv["bytes_per_launch"],
                      "avg_launch_us": round(gemv["per_launch_us"], 3)},
+        "gemv_concatenated": gemv["concatenated"],
     }
     del gemv
     torch.cuda.empty_cache()

@@ -84,6 +84,15 @@ def test_gemv_shapes(session, oracle, gpu, m, n, k):
     check(oracle, got, oracle.q4gemm_packed(c.x, c.packed, c.scales), label=f"gemv {m}x{n}x{k}")
 
 
+def test_gemv_many_columns_per_wavefront(session, oracle, gpu):
+    """Large N makes each wavefront own the maximum run of 64 columns (the concatenated-weights case)."""
+    m, n, k = 1, 200_003, 256
+    note(f"gemv m={m} n={n} k={k}")
+    c = make_case(m, n, k)
+    got = session.q4gemm_values(c.x, c.packed, c.scales, m, n, k)
+    check(oracle, got, oracle.q4gemm_packed(c.x, c.packed, c.scales, threads=threads()), label="gemv many columns")
+
+
 @pytest.mark.parametrize("m,n,k", [(5, 1, 32), (5, 17, 96), (16, 256, 256), (17, 300, 1024), (32, 64, 64),
                                    (16, 4096, 4064), (9, 40, 128), (31, 33, 384),
                                    (33, 129, 160), (100, 300, 512), (130, 260, 1056), (256, 512, 2048)])
