@@ -114,6 +114,23 @@ int spaceslug_q4gemm_lora_device(const float* d_x, const uint8_t* d_w_packed,
 /* Device-resident weights (handle pattern of tiny_forward_persistent.h:556 and
  * .cpp:4751-4800, 5373-5378): uploads w_packed/w_scales once so repeated
  * projections (backend.py:1719-1735 issues five per token) do not re-stage them. */
+/* fp32 -> int4 group-32 quantizer writing the packed layout above (no counterpart
+ * in the reference, whose int4 weights come only from its test generators,
+ * test_q4gemm.cpp:71-80; it is what lets real fp32 checkpoints feed the kernels).
+ * w is float[k][n] row-major, the orientation of the reference's logical B
+ * (test_q4gemm.cpp:16). Per column n and 32-value group g: m = the value of
+ * largest magnitude (first in k order on ties), scale = -m/8, nibble =
+ * clamp(rint(w/scale), -8, 7) with IEEE division and round-to-nearest-even; an
+ * all-zero group gets scale 0 and zero nibbles. Needs k % 32 == 0 and
+ * k/32 <= 65535; non-finite weights return 1. Synchronous host pointers. */
+int spaceslug_q4_quantize(const float* w, uint8_t* w_packed, float* w_scales, uint32_t n, uint32_t k);
+
+/* Device-pointer, stream-ordered variant of spaceslug_q4_quantize. d_w_packed must
+ * be 16-byte aligned. Enqueues only and does not reject non-finite weights: a
+ * group holding a NaN or an infinity gets a NaN scale and zero nibbles. */
+int spaceslug_q4_quantize_device(const float* d_w, uint8_t* d_w_packed, float* d_w_scales, uint32_t n,
+                                 uint32_t k, void* stream);
+
 typedef struct spaceslug_q4_weight spaceslug_q4_weight;
 
 spaceslug_q4_weight* spaceslug_q4_weight_create(const uint8_t* w_packed, const float* w_scales,

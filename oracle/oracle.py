@@ -56,6 +56,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_compare.argtypes = [_f32p, _f64p, ctypes.c_size_t, ctypes.c_double, _f64p, _f64p,
                                      ctypes.POINTER(ctypes.c_int64), _f64p]
         L.oracle_compare.restype = ctypes.c_size_t
+        L.oracle_q4_quantize.argtypes = [_f32p, ctypes.c_uint32, ctypes.c_uint32, _u8p, _f32p]
+        L.oracle_q4_quantize.restype = ctypes.c_int
     return _lib
 
 
@@ -157,6 +159,17 @@ def q4gemm_lora(a: np.ndarray, packed: np.ndarray, scales: np.ndarray, la: np.nd
     if rc != 0:
         raise ValueError("q4gemm_lora: bad arguments")
     return c
+
+
+def q4_quantize(w: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """fp32 w [K, N] -> (packed uint8 [N, K/2], scales float32 [N, K/32]), the rule of spaceslug_q4_quantize."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    K, N = w.shape
+    packed = np.empty((N, K // 2), dtype=np.uint8)
+    scales = np.empty((N, K // 32), dtype=np.float32)
+    if lib().oracle_q4_quantize(_ptr(w, _f32p), K, N, _ptr(packed, _u8p), _ptr(scales, _f32p)) != 0:
+        raise ValueError("q4_quantize: K must be a multiple of 32")
+    return packed, scales
 
 
 def compare(actual: np.ndarray, expected: np.ndarray, tol: float) -> dict:

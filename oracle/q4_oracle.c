@@ -193,3 +193,40 @@ size_t oracle_compare(const float* actual, const double* expected, size_t n, dou
     if (normwise) *normwise = sqrt(num) / (sqrt(den) > 1e-300 ? sqrt(den) : 1e-300);
     return bad;
 }
+
+int oracle_q4_quantize(const float* w, uint32_t K, uint32_t N, uint8_t* packed, float* scales) {
+    if (!w || !packed || !scales || (K % 32u) != 0u) return 1;
+    const uint32_t G = K / 32u;
+    const size_t half = K / 2u;
+    memset(packed, 0, half * (size_t)N);
+    for (uint32_t n = 0; n < N; ++n) {
+        for (uint32_t g = 0; g < G; ++g) {
+            float m = w[(size_t)(32u * g) * N + n];
+            int finite = isfinite(m);
+            for (uint32_t t = 1; t < 32u; ++t) {
+                const float v = w[(size_t)(32u * g + t) * N + n];
+                if (fabsf(v) > fabsf(m)) m = v;
+                if (!isfinite(v)) finite = 0;
+            }
+            float scale = -m * 0.125f;
+            if (!finite) {
+                scales[(size_t)n * G + g] = NAN;
+                continue;
+            }
+            if (scale == 0.0f) {
+                scales[(size_t)n * G + g] = 0.0f;
+                continue;
+            }
+            scales[(size_t)n * G + g] = scale;
+            for (uint32_t t = 0; t < 32u; ++t) {
+                const uint32_t k = 32u * g + t;
+                float r = rintf(w[(size_t)k * N + n] / scale);
+                if (r < -8.0f) r = -8.0f;
+                if (r > 7.0f) r = 7.0f;
+                const uint32_t nib = (uint32_t)(int)r & 0xFu;
+                packed[(size_t)n * half + (k >> 1)] |= (uint8_t)(nib << ((k & 1u) * 4u));
+            }
+        }
+    }
+    return 0;
+}

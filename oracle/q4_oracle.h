@@ -18,7 +18,10 @@
  *   - python/spaceslug/lora.py:21-23, vulkan-runtime/shaders/lora_delta.comp:2-21,
  *     python/spaceslug/backend.py:794-799       LoRA composition
  * The normal generator (Box-Muller on the same LCG) has no counterpart in the
- * reference; it only shapes synthetic N(mu, sigma) inputs.
+ * reference; it only shapes synthetic N(mu, sigma) inputs. Neither has the
+ * fp32 -> int4 quantizer (oracle_q4_quantize): it restates the rule of this
+ * build's spaceslug_q4_quantize (documented in include/runtime_abi.h) so the
+ * GPU quantizer can be checked bit for bit.
  *
  * Parity pins (tests/test_oracle.py): Numerical Recipes' published LCG
  * sequence; hand-derived nibble bytes from the layout comments; exhaustive
@@ -93,6 +96,13 @@ int oracle_q4gemm_lora_rows(const float* a, const uint8_t* packed, const float* 
  * number of elements over tol. */
 size_t oracle_compare(const float* actual, const double* expected, size_t n, double tol,
                       double* max_rel, double* max_abs, int64_t* first_bad, double* normwise);
+
+/* fp32 w[k][n] -> packed int4 [n][k/2] + scales [n][k/32]: per (column, group of
+ * 32) m = largest-magnitude value (first in k order), scale = -m/8, nibble =
+ * clamp(rint(w/scale), -8, 7); scale 0 and zero nibbles for an all-zero group;
+ * NaN scale and zero nibbles for a group holding a NaN or an infinity. Returns 1
+ * unless k % 32 == 0. */
+int oracle_q4_quantize(const float* w, uint32_t K, uint32_t N, uint8_t* packed, float* scales);
 
 #ifdef __cplusplus
 }

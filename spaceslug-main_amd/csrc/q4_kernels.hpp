@@ -46,6 +46,11 @@ hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float*
                          uint32_t n, uint32_t k, const float* la, const float* lb, uint32_t rank,
                          float lora_scale, void* workspace, hipStream_t stream);
 
+// fp32 w[k][n] (row-major) -> packed int4 weights [n][k/2] and scales [n][k/32]; k % 32 == 0 and
+// k / 32 <= 65535 (checked by the caller). Rule at q4_quantize.hip.
+hipError_t launch_q4_quantize(const float* w, uint8_t* w_packed, float* w_scales, uint32_t n, uint32_t k,
+                              hipStream_t stream);
+
 // fp32 C = A * B, row-major, m % 64 == 0, n % 64 == 0, k % 32 == 0 (checked by the caller).
 hipError_t launch_sgemm(const float* a, const float* b, float* c, uint32_t m, uint32_t n,
                         uint32_t k, hipStream_t stream);

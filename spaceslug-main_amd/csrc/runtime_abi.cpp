@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include <climits>
+#include <cmath>
 #include <cstdint>
 #include <cstring>
 #include <exception>
@@ -377,6 +378,54 @@ void spaceslug_q4_weight_destroy(spaceslug_q4_weight* weight) {
     if (weight->d_scales) (void)hipFree(weight->d_scales);
     if (prev >= 0 && prev != weight->device) (void)hipSetDevice(prev);
     delete weight;
+}
+
+int spaceslug_q4_quantize(const float* w, uint8_t* w_packed, float* w_scales, uint32_t n, uint32_t k) {
+    if (!w || !w_packed || !w_scales) return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4_quantize: null pointer");
+    if (!dims_ok(1, n, k) || k / spaceslug::kGroup > 65535u)
+        return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4_quantize: need n>=1, k>=32, k%32==0, k/32<=65535");
+    const size_t count = static_cast<size_t>(n) * k;
+    for (size_t i = 0; i < count; ++i)
+        if (!std::isfinite(w[i])) return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4_quantize: non-finite weight");
+    try {
+        (void)current_device();
+        StagingArena arena({count * sizeof(float), bytes_w(n, k), bytes_s(n, k)});
+        check(hipMemcpy(arena.slice<float>(0), w, count * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy (w)");
+        check(spaceslug::launch_q4_quantize(arena.slice<float>(0), arena.slice<uint8_t>(1), arena.slice<float>(2), n, k,
+                                            nullptr),
+              "quantize launch");
+        check(hipMemcpy(w_packed, arena.slice<uint8_t>(1), bytes_w(n, k), hipMemcpyDeviceToHost), "hipMemcpy (packed)");
+        check(hipMemcpy(w_scales, arena.slice<float>(2), bytes_s(n, k), hipMemcpyDeviceToHost), "hipMemcpy (scales)");
+        return ok();
+    } catch (const HipError& e) {
+        return from_hip(e);
+    } catch (const std::exception& e) {
+        return fail(SPACESLUG_ERR_DEVICE, e.what());
+    } catch (...) {
+        return fail(SPACESLUG_ERR_DEVICE, "spaceslug_q4_quantize: unknown exception");
+    }
+}
+
+int spaceslug_q4_quantize_device(const float* d_w, uint8_t* d_w_packed, float* d_w_scales, uint32_t n, uint32_t k,
+                                 void* stream) {
+    if (!d_w || !d_w_packed || !d_w_scales)
+        return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4_quantize_device: null pointer");
+    if (!dims_ok(1, n, k) || k / spaceslug::kGroup > 65535u)
+        return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4_quantize_device: need n>=1, k>=32, k%32==0, k/32<=65535");
+    if (!aligned(d_w_packed, 16) || !aligned(d_w, 4) || !aligned(d_w_scales, 4))
+        return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4_quantize_device: d_w_packed must be 16-byte aligned");
+    try {
+        (void)current_device();
+        check(spaceslug::launch_q4_quantize(d_w, d_w_packed, d_w_scales, n, k, static_cast<hipStream_t>(stream)),
+              "quantize launch");
+        return ok();
+    } catch (const HipError& e) {
+        return from_hip(e);
+    } catch (const std::exception& e) {
+        return fail(SPACESLUG_ERR_DEVICE, e.what());
+    } catch (...) {
+        return fail(SPACESLUG_ERR_DEVICE, "spaceslug_q4_quantize_device: unknown exception");
+    }
 }
 
 int spaceslug_q4gemm_run(const spaceslug_q4_weight* weight, const float* x, float* y, uint32_t m) {

@@ -172,6 +172,12 @@ class BackendSession:
                 lib.spaceslug_q4_weight_destroy.restype = None
                 lib.spaceslug_q4gemm_run.argtypes = [ctypes.c_void_p, _f32p, _f32p, _u32]
                 lib.spaceslug_q4gemm_run.restype = ctypes.c_int
+            if hasattr(lib, "spaceslug_q4_quantize"):
+                lib.spaceslug_q4_quantize.argtypes = [_f32p, _u8p, _f32p, _u32, _u32]
+                lib.spaceslug_q4_quantize.restype = ctypes.c_int
+            if hasattr(lib, "spaceslug_q4_quantize_device"):
+                lib.spaceslug_q4_quantize_device.argtypes = [ctypes.c_void_p] * 3 + [_u32, _u32, ctypes.c_void_p]
+                lib.spaceslug_q4_quantize_device.restype = ctypes.c_int
             self._library = lib
         return self._library
 
@@ -311,6 +317,27 @@ class BackendSession:
                                                 ctypes.c_void_p(d_lora_b), ctypes.c_void_p(d_y), m, n, k, rank,
                                                 float(scale), ctypes.c_void_p(stream))
         self._check(code, "q4gemm_lora_device")
+
+    # -- fp32 -> int4 group-32 quantizer ----------------------------------------------------------
+    def q4_quantize_values(self, w: Any, n: int, k: int) -> tuple[np.ndarray, np.ndarray]:
+        """fp32 w[k][n] (row-major) -> (packed uint8 [n, k/2], scales float32 [n, k/32]) through
+        spaceslug_q4_quantize (rule in include/runtime_abi.h)."""
+        lib = self._require("spaceslug_q4_quantize")
+        if k % 32 or n <= 0 or k <= 0:
+            raise BackendError("native q4_quantize needs n >= 1 and k % 32 == 0")
+        ww = _f32(w, k * n, "w")
+        packed = np.empty((n, k // 2), dtype=np.uint8)
+        scales = np.empty((n, k // 32), dtype=np.float32)
+        self._check(lib.spaceslug_q4_quantize(ww.ctypes.data_as(_f32p), packed.ctypes.data_as(_u8p),
+                                              scales.ctypes.data_as(_f32p), n, k), "q4_quantize")
+        return packed, scales
+
+    def q4_quantize_device(self, d_w: int, d_w_packed: int, d_w_scales: int, n: int, k: int,
+                           stream: int = 0) -> None:
+        lib = self._require("spaceslug_q4_quantize_device")
+        code = lib.spaceslug_q4_quantize_device(ctypes.c_void_p(d_w), ctypes.c_void_p(d_w_packed),
+                                                ctypes.c_void_p(d_w_scales), n, k, ctypes.c_void_p(stream))
+        self._check(code, "q4_quantize_device")
 
     # -- helpers -----------------------------------------------------------------------------------
     @staticmethod

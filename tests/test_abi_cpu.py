@@ -41,7 +41,7 @@ def test_header_declares_the_expected_surface():
     for required in ("spaceslug_vector_add", "spaceslug_sgemm", "spaceslug_q4gemm", "spaceslug_q4gemm_lora",
                      "spaceslug_q4gemm_device", "spaceslug_q4gemm_lora_device", "spaceslug_q4_weight_create",
                      "spaceslug_q4_weight_destroy", "spaceslug_q4gemm_run", "spaceslug_q4gemm_capability",
-                     "spaceslug_last_error"):
+                     "spaceslug_last_error", "spaceslug_q4_quantize", "spaceslug_q4_quantize_device"):
         assert required in names
 
 
@@ -162,6 +162,8 @@ def test_no_cpu_fallback_without_device(lib):
     err = ctypes.c_float()
     a = np.zeros(64 * 64, np.float32)
     assert lib.spaceslug_sgemm(_p(a), _p(a), _p(a), 64, 64, 32, ctypes.byref(err)) == 2
+    packed = np.zeros(64 * 32, np.uint8)
+    assert lib.spaceslug_q4_quantize(_p(a), _p(packed, u8p), _p(a), 64, 64) == 2
 
 
 # -- host shim (spaceslug_amd.BackendSession) --------------------------------------------------------
