@@ -1,0 +1,35 @@
+"""The C-ABI from a compiled C++ caller (spaceslug-main_amd/examples/runtime_abi_client.cpp), built with g++
+against include/runtime_abi.h and the runtime library the way a C++ host would link it."""
+from __future__ import annotations
+
+import subprocess
+from pathlib import Path
+
+import pytest
+
+REPO = Path(__file__).resolve().parent.parent
+SRC = REPO / "spaceslug-main_amd" / "examples" / "runtime_abi_client.cpp"
+
+
+def build_client(runtime_lib_path: Path, out: Path) -> Path:
+    lib_dir = runtime_lib_path.parent
+    subprocess.run(["g++", "-std=c++17", "-O2", f"-I{REPO / 'include'}", str(SRC), f"-L{lib_dir}",
+                    "-lspaceslug_runtime", f"-Wl,-rpath,{lib_dir}", "-o", str(out)], check=True)
+    return out
+
+
+def test_client_builds_and_runs_without_gpu(runtime_lib_path, tmp_path):
+    exe = build_client(runtime_lib_path, tmp_path / "client")
+    r = subprocess.run([str(exe), "--allow-no-device"], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "vector_add: PASS" in r.stdout
+
+
+@pytest.mark.gpu
+def test_client_int4_call_on_gpu(runtime_lib_path, gpu, tmp_path):
+    exe = build_client(runtime_lib_path, tmp_path / "client")
+    print("[gpu-case] C++ client", flush=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    print(r.stdout, flush=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "q4gemm: PASS" in r.stdout

@@ -306,3 +306,47 @@ def test_split_k_calls_on_two_streams(session, oracle, gpu):
     torch.cuda.synchronize()
     for i in range(2):
         check(oracle, ys[i].cpu().numpy(), want[i], label=f"stream {i}")
+
+
+@pytest.mark.parametrize("m", [1, 16])
+def test_projection_chain_in_a_hip_graph(session, oracle, gpu, m):
+    """Two chained projections (y1 = x W1, y2 = y1 W2) captured once in a HIP graph through the device entry
+    point and replayed with new inputs: every replay equals the eager chain bit for bit. Shapes that need no
+    library workspace (decode GEMV, small-M kernel) are capturable."""
+    import torch
+
+    note(f"graph chain m={m}")
+    k1, n1, n2 = 512, 1024, 384
+    c1 = make_case(m, n1, k1, seed_b=0x51, seed_s=0x52)
+    c2 = make_case(m, n2, n1, seed_b=0x61, seed_s=0x62)
+    w1, s1 = to_dev(c1.packed, torch), to_dev(c1.scales, torch)
+    w2, s2 = to_dev(c2.packed, torch), to_dev(c2.scales, torch)
+    x = to_dev(c1.x, torch)
+    y1 = torch.empty((m, n1), dtype=torch.float32, device="cuda:0")
+    y2 = torch.empty((m, n2), dtype=torch.float32, device="cuda:0")
+
+    def chain(stream):
+        session.q4gemm_device(x.data_ptr(), w1.data_ptr(), s1.data_ptr(), y1.data_ptr(), m, n1, k1, stream)
+        session.q4gemm_device(y1.data_ptr(), w2.data_ptr(), s2.data_ptr(), y2.data_ptr(), m, n2, n1, stream)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        chain(side.cuda_stream)  # warm-up outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        chain(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        x.copy_(torch.from_numpy(c1.x * np.float32(1.0 + 0.25 * rep)).to("cuda:0"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = y2.clone()
+        chain(torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert torch.equal(got, y2), f"replay {rep} differs from the eager chain"
+    want1 = oracle.q4gemm_packed(c1.x * np.float32(1.5), c1.packed, c1.scales)
+    check(oracle, y1.cpu().numpy(), want1, label=f"graph chain m={m} layer 1")
