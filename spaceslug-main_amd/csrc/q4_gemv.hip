@@ -20,6 +20,8 @@
 //     lane partials of a column are summed with DPP row operations plus two
 //     row broadcasts, and the factor 16 restored exactly at the end.
 // K larger than one chunk (64 * SPC groups per lane pass) is walked in chunks.
+// One row with K <= 4096 takes the software-pipelined integer kernel below
+// (q4_gemv_pipe_kernel), which reads the weights in the same mapping.
 #include "q4_device.hpp"
 #include "q4_kernels.hpp"
 
@@ -205,14 +207,72 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const float* x,  
     }
 }
 
-// Software-pipelined single-row decode (M = 1, K <= 64 * SPC * 32): each wavefront
-// owns CPB = D * ITERS consecutive columns and keeps D columns of loads in flight,
-// computing column i while columns i+1 .. i+D stream in. x is staged once per
-// workgroup in LDS and held in registers for all of the wavefront's columns.
+// Software-pipelined single-row decode (M = 1, K <= 4096) in integer arithmetic.
+//
+// x is recoded once per workgroup. For each 32-value group g, with e_g the
+// exponent for which max|x| < 2^e_g, X_k = rint(x_k * 2^(30 - e_g)) is an integer
+// with |X_k| <= 2^30 that holds x_k to within 2^(e_g - 31), at most 2^-30 of the
+// group's largest magnitude (finer than fp32's own rounding of a product of that
+// magnitude, so a group holding an outlier loses nothing against float arithmetic).
+// X_k is written as eight signed base-16 digits d_j in [-8, 7]: with
+// Y = X + 0x88888888 (0 <= Y < 2^32), d_j = (hex digit j of Y) - 8, whose 4-bit two's
+// complement is (hex digit j of Y) xor 8. Digit j of the eight values
+// k = 8w .. 8w + 7 of a group is packed into one word, nibble t holding k = 8w + t:
+// the layout of the packed weight words. v_dot8_i32_i4 (eight signed 4-bit
+// products plus an int32 add) then takes a weight word and a digit word as they
+// are, with no nibble decoding:
+//   sum_k v_k X_k = 65536 H + L,  H = sum_{j=4..7} 16^(j-4) sum_k v_k d_kj,
+//                                 L = sum_{j=0..3} 16^j     sum_k v_k d_kj,
+// both evaluated by Horner steps (a shift by 4 between digits). Over one group
+// |H|, |L| <= 32 * 8 * 34952 < 2^24, so both are exact in int32 and in float, and
+// 65536 H + L is rounded once (one fma). The group partial
+// (65536 H + L) * 2^(e_g - 30) * s(n, g) is accumulated in fp32 per lane.
+// Cost per 32 nibbles: 32 v_dot8 + 6 shifts + 6 other VALU ops, against 68 for
+// decoding to float (4 x (8 conversions + 1 shift + 8 fma)); the kernel is bound
+// by its per-wavefront VALU time as much as by HBM, so this is what buys speed.
+//
+// Each wavefront owns CPB = D * ITERS consecutive columns and keeps D columns of
+// loads in flight, computing column i while columns i+1 .. i+D stream in.
+constexpr int kXDigits = 8;               // signed base-16 digits per recoded x value
+constexpr int kXFracBits = 30;            // |X| <= 2^30
+constexpr uint32_t kXBias = 0x88888888u;  // 8 in each of the eight digit positions
+
+// 8 x 8 transpose of 4-bit cells: on return nibble t of r[j] is what nibble j of
+// r[t] held (16-bit and 8-bit blocks by byte permutes, then nibble swaps).
+__device__ __forceinline__ void transpose_nibbles(uint32_t (&r)[8]) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const uint32_t a = r[t], b = r[t + 4];
+        r[t] = __builtin_amdgcn_perm(b, a, 0x05040100u);      // bytes a0 a1 b0 b1
+        r[t + 4] = __builtin_amdgcn_perm(b, a, 0x07060302u);  // bytes a2 a3 b2 b3
+    }
+#pragma unroll
+    for (int t : {0, 1, 4, 5}) {
+        const uint32_t a = r[t], b = r[t + 2];
+        r[t] = __builtin_amdgcn_perm(b, a, 0x06020400u);      // bytes a0 b0 a2 b2
+        r[t + 2] = __builtin_amdgcn_perm(b, a, 0x07030501u);  // bytes a1 b1 a3 b3
+    }
+#pragma unroll
+    for (int t = 0; t < 8; t += 2) {
+        const uint32_t a = r[t], b = r[t + 1];
+        r[t] = (a & 0x0F0F0F0Fu) | ((b << 4) & 0xF0F0F0F0u);
+        r[t + 1] = ((a >> 4) & 0x0F0F0F0Fu) | (b & 0xF0F0F0F0u);
+    }
+}
+
 template <int SPC, int D>
 struct PipeSlot {
     u32x4 wv[SPC];
     float sc[SPC];
+};
+
+// The lane's recoded x: digit j of word w of group slot s at d[s][w * kXDigits + j],
+// and the group's factor 2^(e_g - 30) (0 past K, NaN when the group holds a
+// non-finite value, so that its outputs are NaN).
+template <int SPC>
+struct XDigits {
+    uint32_t d[SPC][4 * kXDigits];
+    float c[SPC];
 };
 
 template <int SPC, int D>
@@ -232,22 +292,33 @@ __device__ __forceinline__ void pipe_issue(PipeSlot<SPC, D>& slot, const u32x4* 
 }
 
 template <int SPC, int D>
-__device__ __forceinline__ float pipe_column(const PipeSlot<SPC, D>& slot, const float (&xv)[SPC][32],
+__device__ __forceinline__ float pipe_column(const PipeSlot<SPC, D>& slot, const XDigits<SPC>& xd,
                                              const bool (&valid)[SPC]) {
     float acc = 0.0f;
 #pragma unroll
     for (int s = 0; s < SPC; ++s) {
-        float f[32];
+        int hi = 0;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) nibbles_signed_16th(slot.wv[s][w], *reinterpret_cast<float(*)[8]>(&f[8 * w]));
-        float p0 = 0.0f, p1 = 0.0f;
+        for (int j = kXDigits - 1; j >= 4; --j) {
+            if (j < kXDigits - 1) hi *= 16;
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            p0 = fmaf(xv[s][k], f[k], p0);
-            p1 = fmaf(xv[s][16 + k], f[16 + k], p1);
+            for (int w = 0; w < 4; ++w)
+                hi = __builtin_amdgcn_sdot8(static_cast<int>(slot.wv[s][w]), static_cast<int>(xd.d[s][w * kXDigits + j]),
+                                            hi, false);
         }
+        int lo = 0;
+#pragma unroll
+        for (int j = 3; j >= 0; --j) {
+            if (j < 3) lo *= 16;
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+                lo = __builtin_amdgcn_sdot8(static_cast<int>(slot.wv[s][w]), static_cast<int>(xd.d[s][w * kXDigits + j]),
+                                            lo, false);
+        }
+        const float p = fmaf(static_cast<float>(hi), 65536.0f, static_cast<float>(lo));
+        // a lane past K reads a real (clamped) scale, which may be NaN: select, not multiply
         const float sc = valid[s] ? slot.sc[s] : 0.0f;
-        acc = fmaf(sc, p0 + p1, acc);
+        acc = fmaf(sc, p * xd.c[s], acc);
     }
     return wave_reduce_dpp(acc);
 }
@@ -257,10 +328,10 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
                                                                    const u32x4* __restrict__ wq,
                                                                    const float* __restrict__ ws,
                                                                    float* __restrict__ y, int N, int K, int iters) {
-    constexpr int kChunkF4 = 64 * SPC * 8;
-    constexpr int kPerThread = kChunkF4 / kGemvThreads;
-    static_assert(kChunkF4 % kGemvThreads == 0, "x chunk must split evenly over the workgroup");
-    __shared__ f32x4 xs[kChunkF4];
+    constexpr int kGroups = 64 * SPC;  // groups per lane pass: K <= 32 * kGroups
+    static_assert(kGroups * 2 == kGemvThreads, "x is recoded by two threads per group");
+    __shared__ __align__(16) uint32_t xds[kGroups * 4 * kXDigits];
+    __shared__ float xcs[kGroups];
     const int lane = threadIdx.x & 63;
     const int wave =
         __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)));
@@ -270,12 +341,15 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
     const int col0 = wave * cpb;
     const int G = K >> 5;
 
-    // x first (coalesced), then the first D columns, all before any wait.
-    const int c4_last = (K >> 2) - 1;
-    f32x4 xr[kPerThread];
+    // x first (thread t recodes half t & 1, 16 values, of group t >> 1), then the
+    // first D columns, all before any wait.
+    const int rg = threadIdx.x >> 1, rh = threadIdx.x & 1;
+    f32x4 xr[4];
+    {
+        const f32x4* src = reinterpret_cast<const f32x4*>(x + static_cast<size_t>(min(rg, G - 1)) * 32 + rh * 16);
 #pragma unroll
-    for (int i = 0; i < kPerThread; ++i)
-        xr[i] = reinterpret_cast<const f32x4*>(x)[min(static_cast<int>(threadIdx.x) + i * kGemvThreads, c4_last)];
+        for (int i = 0; i < 4; ++i) xr[i] = src[i];
+    }
     asm volatile("" ::: "memory");
     uint32_t off16[SPC], off4[SPC];
     bool valid[SPC];
@@ -296,25 +370,53 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
     }
     asm volatile("" ::: "memory");
 
+    {
+        float m = 0.0f, fin = 1.0f;
 #pragma unroll
-    for (int i = 0; i < kPerThread; ++i) {
-        const int c = static_cast<int>(threadIdx.x) + i * kGemvThreads;
-        const int g = c >> 3, q = c & 7;
-        xs[(g << 3) + (q ^ (g & 7))] = xr[i];
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                m = fmaxf(m, fabsf(xr[i][c]));  // maxNum: a NaN is caught by fin
+                fin = __builtin_isfinite(xr[i][c]) ? fin : 0.0f;
+            }
+        m = fmaxf(m, dpp_src<0xB1>(m));  // the partner thread holds the group's other half
+        fin = fminf(fin, dpp_src<0xB1>(fin));
+        int e = 0;
+        (void)frexpf(m, &e);  // m < 2^e (e = 0 for m = 0)
+        const bool finite = fin > 0.5f;
+        uint32_t r[2][8];
+#pragma unroll
+        for (int w = 0; w < 2; ++w)
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const float v = xr[(8 * w + t) >> 2][t & 3];
+                const int X = finite ? static_cast<int>(rintf(ldexpf(v, kXFracBits - e))) : 0;
+                r[w][t] = (static_cast<uint32_t>(X) + kXBias) ^ 0x88888888u;  // Y, each digit xor 8
+            }
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            transpose_nibbles(r[w]);
+#pragma unroll
+            for (int j = 0; j < kXDigits; ++j) xds[rg * 4 * kXDigits + (2 * rh + w) * kXDigits + j] = r[w][j];
+        }
+        if (rh == 0)
+            xcs[rg] = rg >= G ? 0.0f : (finite ? ldexpf(1.0f, e - kXFracBits) : __builtin_nanf(""));
     }
     __syncthreads();
-    float xv[SPC][32];
+    XDigits<SPC> xd;
 #pragma unroll
     for (int s = 0; s < SPC; ++s) {
         const int gl = 64 * s + lane;
+        const u32x4* src = reinterpret_cast<const u32x4*>(xds + gl * 4 * kXDigits);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const f32x4 t = xs[(gl << 3) + (q ^ (gl & 7))];
-            xv[s][4 * q + 0] = t[0];
-            xv[s][4 * q + 1] = t[1];
-            xv[s][4 * q + 2] = t[2];
-            xv[s][4 * q + 3] = t[3];
+        for (int q = 0; q < kXDigits; ++q) {
+            const u32x4 t = src[q];
+            xd.d[s][4 * q + 0] = t[0];
+            xd.d[s][4 * q + 1] = t[1];
+            xd.d[s][4 * q + 2] = t[2];
+            xd.d[s][4 * q + 3] = t[3];
         }
+        xd.c[s] = xcs[gl];
     }
 
     // Steady state: compute slot d (column i), then refill it with column i + D.
@@ -323,7 +425,7 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
     for (int it = 0; it + 1 < iters; ++it) {
 #pragma unroll
         for (int d = 0; d < D; ++d, ++i) {
-            const float t = pipe_column<SPC, D>(slot[d], xv, valid);
+            const float t = pipe_column<SPC, D>(slot[d], xd, valid);
             result = lane == i ? t : result;
             pipe_issue<SPC, D>(slot[d], wq, ws, col0 + i + D, N, G, off16, off4);
             // Keep the next slot's arithmetic below this refill: otherwise the scheduler
@@ -333,11 +435,11 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
     }
 #pragma unroll
     for (int d = 0; d < D; ++d, ++i) {
-        const float t = pipe_column<SPC, D>(slot[d], xv, valid);
+        const float t = pipe_column<SPC, D>(slot[d], xd, valid);
         result = lane == i ? t : result;
     }
     // lane c holds column col0 + c: one coalesced store of the wavefront's run
-    if (lane < cpb && col0 + lane < N) y[col0 + lane] = result * kSixteenthsUnit;
+    if (lane < cpb && col0 + lane < N) y[col0 + lane] = result;
 }
 
 template <int M, int SPC, int CPW>
@@ -346,15 +448,20 @@ hipError_t launch_rows(const float* x, const uint8_t* w_packed, const float* w_s
     const size_t waves = (static_cast<size_t>(n) + CPW - 1) / CPW;
     const size_t blocks = (waves + kGemvThreads / 64 - 1) / (kGemvThreads / 64);
     const bool single = (k / kGroup) <= static_cast<uint32_t>(64 * SPC);
-    if (single) {
-        hipLaunchKernelGGL((q4_gemv_kernel<M, SPC, CPW, true>), dim3(static_cast<unsigned>(blocks)),
-                           dim3(kGemvThreads), 0, stream, x, reinterpret_cast<const u32x4*>(w_packed), w_scales, y,
-                           static_cast<int>(n), static_cast<int>(k));
-    } else {
-        hipLaunchKernelGGL((q4_gemv_kernel<M, SPC, CPW, false>), dim3(static_cast<unsigned>(blocks)),
-                           dim3(kGemvThreads), 0, stream, x, reinterpret_cast<const u32x4*>(w_packed), w_scales, y,
-                           static_cast<int>(n), static_cast<int>(k));
+    // One row reaches this kernel only for K > 4096 (the pipelined kernel takes the rest),
+    // so its single-chunk form is never instantiated.
+    if constexpr (M > 1) {
+        if (single) {
+            hipLaunchKernelGGL((q4_gemv_kernel<M, SPC, CPW, true>), dim3(static_cast<unsigned>(blocks)),
+                               dim3(kGemvThreads), 0, stream, x, reinterpret_cast<const u32x4*>(w_packed), w_scales, y,
+                               static_cast<int>(n), static_cast<int>(k));
+            return hipGetLastError();
+        }
     }
+    if (single) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((q4_gemv_kernel<M, SPC, CPW, false>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(kGemvThreads), 0, stream, x, reinterpret_cast<const u32x4*>(w_packed), w_scales, y,
+                       static_cast<int>(n), static_cast<int>(k));
     return hipGetLastError();
 }
 

@@ -118,9 +118,64 @@ def test_extreme_nibbles_and_scales(session, oracle, gpu, m):
     packed = oracle.pack_q4(b)
     got = session.q4gemm_values(c.x, packed, scales, m, n, k)
     check(oracle, got, oracle.q4gemm_ref(c.x, b, scales), label="extreme")
-    # An all-zero column is exactly 0 on the MFMA path; the decode path subtracts the
-    # offset-binary bias sum(x)/64 and leaves rounding residue of order 2^-24 * sum|x|.
-    assert np.abs(got[:, 7]).max() <= 2.0**-20 * np.abs(c.x).sum(axis=1).max()
+    # every path decodes signed nibbles (no offset to cancel): an all-zero column is exactly 0
+    assert np.all(got[:, 7] == 0.0)
+
+
+def magnitude_stress_x(x: np.ndarray, huge: bool) -> np.ndarray:
+    x = x.copy()
+    x[:, 0:32] = 0.0
+    x[:, 32:64] *= 1e-41                               # subnormal floats
+    if huge:
+        x[:, 64:96] *= 1e30
+    x[:, 96:128] *= 1e-3
+    x[:, 100] = 1000.0                                 # one outlier in a group of small values
+    x[:, 128:160] = np.float32(2.0) ** np.arange(-8, 24, dtype=np.float32)  # max exactly 2^23
+    x[:, 160:192] = -np.abs(x[:, 160:192])
+    x[:, 160] = -7.5                                   # negative extreme
+    return x
+
+
+@pytest.mark.parametrize("k", [4096, 352])
+def test_one_row_x_groups_of_very_different_magnitude(session, oracle, gpu, k):
+    """The one-row kernel recodes x per 32-value group against the group's largest
+    magnitude and sums each group exactly in integers: groups of zeros, subnormals,
+    1e30, one outlier, exact powers of two and a negative extreme all meet the 1e-5 bar,
+    including columns where the 1e30 group's terms cancel to a small fraction of their size."""
+    note(f"x group magnitudes m=1 k={k}")
+    n = 300
+    c = make_case(1, n, k)
+    x = magnitude_stress_x(c.x, huge=True)
+    got = session.q4gemm_values(x, c.packed, c.scales, 1, n, k)
+    check(oracle, got, oracle.q4gemm_packed(x, c.packed, c.scales, threads=threads()), label="x magnitudes")
+
+
+@pytest.mark.parametrize("m,k", [(2, 4096), (24, 512)])
+def test_float_paths_x_groups_of_very_different_magnitude(session, oracle, gpu, m, k):
+    """The same groups on the multi-row paths, which form products in fp32, without the 1e30
+    group: there, cancellation among terms of that size is rounded at 2^-24 of the terms, as in
+    any fp32 GEMM, and can exceed 1e-5 of the (much smaller) result."""
+    note(f"x group magnitudes m={m} k={k}")
+    n = 300
+    c = make_case(m, n, k)
+    x = magnitude_stress_x(c.x, huge=False)
+    got = session.q4gemm_values(x, c.packed, c.scales, m, n, k)
+    check(oracle, got, oracle.q4gemm_packed(x, c.packed, c.scales, threads=threads()), label="x magnitudes")
+
+
+@pytest.mark.parametrize("m", [1, 3, 24])
+def test_nan_in_x_gives_nan_outputs(session, oracle, gpu, m):
+    """A NaN in row r of x makes every output of row r NaN, as in the double reference."""
+    note(f"nan in x m={m}")
+    n, k = 64, 512
+    c = make_case(m, n, k)
+    x = c.x.copy()
+    x[0, 77] = np.nan
+    got = session.q4gemm_values(x, c.packed, c.scales, m, n, k)
+    assert np.all(np.isnan(got[0]))
+    if m > 1:
+        assert np.all(np.isfinite(got[1:]))
+        check(oracle, got[1:], oracle.q4gemm_packed(x[1:], c.packed, c.scales), label="rows without nan")
 
 
 def test_unit_vectors_select_dequantized_rows(session, oracle, gpu):
