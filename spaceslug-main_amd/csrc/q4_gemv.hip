@@ -236,6 +236,8 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const float* x,  
 constexpr int kXDigits = 8;               // signed base-16 digits per recoded x value
 constexpr int kXFracBits = 30;            // |X| <= 2^30
 constexpr uint32_t kXBias = 0x88888888u;  // 8 in each of the eight digit positions
+constexpr int kBufferFlags = 0x00020000;   // buffer resource word 3: 32-bit data format
+constexpr int kNontemporal = 2;            // buffer load cache policy: nt
 
 // 8 x 8 transpose of 4-bit cells: on return nibble t of r[j] is what nibble j of
 // r[t] held (16-bit and 8-bit blocks by byte permutes, then nibble swaps).
@@ -260,7 +262,7 @@ __device__ __forceinline__ void transpose_nibbles(uint32_t (&r)[8]) {
     }
 }
 
-template <int SPC, int D>
+template <int SPC>
 struct PipeSlot {
     u32x4 wv[SPC];
     float sc[SPC];
@@ -275,25 +277,31 @@ struct XDigits {
     float c[SPC];
 };
 
-template <int SPC, int D>
-__device__ __forceinline__ void pipe_issue(PipeSlot<SPC, D>& slot, const u32x4* __restrict__ wq,
+// One column's weights and scales through buffer resources whose base is the
+// column (scalar arithmetic only) and whose size is one column: the lane offsets
+// are fixed for the whole kernel, and a lane whose group lies past K reads zeros
+// (the buffer range check), so it contributes nothing without a per-column select.
+// Weights and scales are read exactly once: nontemporal (aux 2) keeps them from
+// displacing x and each other in the caches.
+template <int SPC>
+__device__ __forceinline__ void pipe_issue(PipeSlot<SPC>& slot, const u32x4* __restrict__ wq,
                                            const float* __restrict__ ws, int col, int N, int G,
                                            const uint32_t (&off16)[SPC], const uint32_t (&off4)[SPC]) {
     const size_t base = static_cast<size_t>(min(col, N - 1)) * G;
-    const char* wcol = reinterpret_cast<const char*>(wq + base);
-    const char* scol = reinterpret_cast<const char*>(ws + base);
-    // Weights and scales are read exactly once: nontemporal loads keep them from
-    // displacing x and each other in the caches (measured 8.2 -> 7.7 us per call).
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<u32x4*>(wq + base), 0, G * 16, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(ws + base), 0, G * 4, kBufferFlags);
 #pragma unroll
     for (int s = 0; s < SPC; ++s) {
-        slot.wv[s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wcol + off16[s]));
-        slot.sc[s] = __builtin_nontemporal_load(reinterpret_cast<const float*>(scol + off4[s]));
+        slot.wv[s] = __builtin_amdgcn_raw_buffer_load_b128(rw, off16[s], 0, kNontemporal);
+        slot.sc[s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, off4[s], 0, kNontemporal));
     }
 }
 
-template <int SPC, int D>
-__device__ __forceinline__ float pipe_column(const PipeSlot<SPC, D>& slot, const XDigits<SPC>& xd,
-                                             const bool (&valid)[SPC]) {
+// The lane's share of one column (not yet summed over the wavefront).
+template <int SPC>
+__device__ __forceinline__ float pipe_partial(const PipeSlot<SPC>& slot, const XDigits<SPC>& xd) {
     float acc = 0.0f;
 #pragma unroll
     for (int s = 0; s < SPC; ++s) {
@@ -316,11 +324,9 @@ __device__ __forceinline__ float pipe_column(const PipeSlot<SPC, D>& slot, const
                                             lo, false);
         }
         const float p = fmaf(static_cast<float>(hi), 65536.0f, static_cast<float>(lo));
-        // a lane past K reads a real (clamped) scale, which may be NaN: select, not multiply
-        const float sc = valid[s] ? slot.sc[s] : 0.0f;
-        acc = fmaf(sc, p * xd.c[s], acc);
+        acc = fmaf(slot.sc[s], p * xd.c[s], acc);
     }
-    return wave_reduce_dpp(acc);
+    return acc;
 }
 
 template <int SPC, int D>
@@ -352,19 +358,15 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
     }
     asm volatile("" ::: "memory");
     uint32_t off16[SPC], off4[SPC];
-    bool valid[SPC];
 #pragma unroll
     for (int s = 0; s < SPC; ++s) {
-        const int g = 64 * s + lane;
-        valid[s] = g < G;
-        const uint32_t gc = static_cast<uint32_t>(min(g, G - 1));
-        off16[s] = gc * 16u;
-        off4[s] = gc * 4u;
+        off16[s] = static_cast<uint32_t>(64 * s + lane) * 16u;  // past K: beyond the buffer, reads 0
+        off4[s] = static_cast<uint32_t>(64 * s + lane) * 4u;
     }
-    PipeSlot<SPC, D> slot[D];
+    PipeSlot<SPC> slot[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-        pipe_issue<SPC, D>(slot[d], wq, ws, col0 + d, N, G, off16, off4);
+        pipe_issue<SPC>(slot[d], wq, ws, col0 + d, N, G, off16, off4);
         // slot by slot, as in the steady state, so the loop's load counts line up
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -419,15 +421,17 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
         xd.c[s] = xcs[gl];
     }
 
-    // Steady state: compute slot d (column i), then refill it with column i + D.
+    // Steady state: compute slot d (column i), then refill it with column i + D. (Reducing
+    // four columns at once with fewer instructions measured slower: the wavefront then
+    // waits out one long dependent chain per four columns.)
     float result = 0.0f;
     int i = 0;
     for (int it = 0; it + 1 < iters; ++it) {
 #pragma unroll
         for (int d = 0; d < D; ++d, ++i) {
-            const float t = pipe_column<SPC, D>(slot[d], xd, valid);
+            const float t = wave_reduce_dpp(pipe_partial<SPC>(slot[d], xd));
             result = lane == i ? t : result;
-            pipe_issue<SPC, D>(slot[d], wq, ws, col0 + i + D, N, G, off16, off4);
+            pipe_issue<SPC>(slot[d], wq, ws, col0 + i + D, N, G, off16, off4);
             // Keep the next slot's arithmetic below this refill: otherwise the scheduler
             // interleaves slots and must wait for every outstanding load first.
             __builtin_amdgcn_sched_barrier(0);
@@ -435,7 +439,7 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
     }
 #pragma unroll
     for (int d = 0; d < D; ++d, ++i) {
-        const float t = pipe_column<SPC, D>(slot[d], xd, valid);
+        const float t = wave_reduce_dpp(pipe_partial<SPC>(slot[d], xd));
         result = lane == i ? t : result;
     }
     // lane c holds column col0 + c: one coalesced store of the wavefront's run
