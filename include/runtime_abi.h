@@ -111,9 +111,6 @@ int spaceslug_q4gemm_lora_device(const float* d_x, const uint8_t* d_w_packed,
                                  const float* d_lora_b, float* d_y, uint32_t m, uint32_t n,
                                  uint32_t k, uint32_t rank, float scale, void* stream);
 
-/* Device-resident weights (handle pattern of tiny_forward_persistent.h:556 and
- * .cpp:4751-4800, 5373-5378): uploads w_packed/w_scales once so repeated
- * projections (backend.py:1719-1735 issues five per token) do not re-stage them. */
 /* fp32 -> int4 group-32 quantizer writing the packed layout above (no counterpart
  * in the reference, whose int4 weights come only from its test generators,
  * test_q4gemm.cpp:71-80; it is what lets real fp32 checkpoints feed the kernels).
@@ -131,6 +128,9 @@ int spaceslug_q4_quantize(const float* w, uint8_t* w_packed, float* w_scales, ui
 int spaceslug_q4_quantize_device(const float* d_w, uint8_t* d_w_packed, float* d_w_scales, uint32_t n,
                                  uint32_t k, void* stream);
 
+/* Device-resident weights (handle pattern of tiny_forward_persistent.h:556 and
+ * .cpp:4751-4800, 5373-5378): uploads w_packed/w_scales once so repeated
+ * projections (backend.py:1719-1735 issues five per token) do not re-stage them. */
 typedef struct spaceslug_q4_weight spaceslug_q4_weight;
 
 spaceslug_q4_weight* spaceslug_q4_weight_create(const uint8_t* w_packed, const float* w_scales,
@@ -139,6 +139,46 @@ void spaceslug_q4_weight_destroy(spaceslug_q4_weight* weight);
 
 /* Synchronous host x/y against a weight handle: y[m][n] = x[m][k] * dequant(W). */
 int spaceslug_q4gemm_run(const spaceslug_q4_weight* weight, const float* x, float* y, uint32_t m);
+
+/* Retained projection chain: a fixed sequence of device-pointer projections recorded
+ * once into one HIP graph and replayed with one launch, with no host round trip and
+ * no per-call planning between the steps. Replaces the reference's retained
+ * command buffers (vulkan-runtime/src/exec/engine.h:85-101, recordImmutable /
+ * submitImmutable: "retain fully recorded command buffers and resubmit without
+ * re-recording") and the persistent tiny forward's handle pattern
+ * (tiny_forward_persistent.h:556-558). A step holds the arguments of one
+ * spaceslug_q4gemm_device call, or of spaceslug_q4gemm_lora_device when d_lora_a is
+ * not NULL; a step may read what an earlier step wrote (steps run in order). */
+typedef struct spaceslug_q4_step {
+    const float* d_x;          /* [m][k], 16-byte aligned */
+    const uint8_t* d_w_packed; /* [n][k/2], 16-byte aligned */
+    const float* d_w_scales;   /* [n][k/32] */
+    float* d_y;                /* [m][n] */
+    uint32_t m, n, k;
+    const float* d_lora_a;     /* [k][rank], or NULL for no LoRA term */
+    const float* d_lora_b;     /* [rank][n] */
+    uint32_t rank;             /* 1..SPACESLUG_Q4_MAX_LORA_RANK when d_lora_a is set */
+    float lora_scale;          /* alpha / rank */
+} spaceslug_q4_step;
+
+typedef struct spaceslug_q4_chain spaceslug_q4_chain;
+
+/* Validates every step as the device entry points do, plans each, records them on
+ * the current device into one graph and instantiates it. The chain owns the
+ * device workspace its steps need, so replays share no memory with other calls.
+ * Addresses are fixed at creation: callers change buffer contents between runs,
+ * never addresses, and must not change them while a replay is in flight
+ * (engine.h:89-91 asks the same of retained command buffers). NULL on failure. */
+spaceslug_q4_chain* spaceslug_q4_chain_create(const spaceslug_q4_step* steps, uint32_t count);
+
+/* Enqueues one replay of the chain on `stream` (hipStream_t as void*, NULL = the
+ * default stream). Replays of one chain must be ordered (one stream, or
+ * synchronised by the caller): they share the chain's workspace. Returns 1 when the
+ * current device is not the chain's. */
+int spaceslug_q4_chain_run(spaceslug_q4_chain* chain, void* stream);
+
+/* Waits for the chain's device, then releases the graph and the workspace. NULL is a no-op. */
+void spaceslug_q4_chain_destroy(spaceslug_q4_chain* chain);
 
 #ifdef __cplusplus
 }

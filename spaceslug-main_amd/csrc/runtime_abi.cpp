@@ -10,6 +10,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 #include <cmath>
 #include <cstdint>
@@ -227,6 +228,46 @@ struct spaceslug_q4_weight {
     float* d_scales;
 };
 
+// A retained chain: the instantiated graph of its steps' launches and the device
+// workspace those launches were recorded against (owned by the chain, so a replay
+// shares no memory with any other call).
+struct spaceslug_q4_chain {
+    int device = -1;
+    uint32_t steps = 0;
+    void* workspace = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+namespace {
+
+// Validation shared by the device entry points and the chain steps; returns an
+// error message, or nullptr when the arguments are acceptable.
+const char* device_call_problem(const float* d_x, const uint8_t* d_w_packed, const float* d_w_scales,
+                                const float* d_lora_a, const float* d_lora_b, float* d_y, uint32_t m, uint32_t n,
+                                uint32_t k, uint32_t rank) {
+    if (!d_x || !d_w_packed || !d_w_scales || !d_y) return "null pointer";
+    if (!dims_ok(m, n, k)) return "need m>=1, n>=1, k%32==0";
+    if (!aligned(d_x, 16) || !aligned(d_w_packed, 16) || !aligned(d_w_scales, 4) || !aligned(d_y, 4))
+        return "misaligned device pointer";
+    if (d_lora_a || d_lora_b) {
+        if (!d_lora_a || !d_lora_b) return "LoRA needs both factors";
+        if (rank == 0 || rank > SPACESLUG_Q4_MAX_LORA_RANK) return "need 1<=rank<=64";
+        if (!aligned(d_lora_a, 4) || !aligned(d_lora_b, 4)) return "misaligned device pointer";
+    }
+    return nullptr;
+}
+
+// Releases whatever a partly built chain holds (the device is current).
+void chain_release(spaceslug_q4_chain* c) {
+    if (c->exec) (void)hipGraphExecDestroy(c->exec);
+    if (c->graph) (void)hipGraphDestroy(c->graph);
+    if (c->workspace) (void)hipFree(c->workspace);
+    delete c;
+}
+
+}  // namespace
+
 extern "C" {
 
 int spaceslug_vector_add(const float* left, const float* right, float* output, size_t count) {
@@ -264,8 +305,9 @@ int spaceslug_sgemm(const float* a, const float* b, float* c, uint32_t m, uint32
 }
 
 const char* spaceslug_q4gemm_capability(void) {
-    return "q4gemm-hip-gfx950 group=32 layout=n-major-lsb-nibble decode=gemv(m<=4) prefill=mfma-f32-16x16x4 "
-           "accumulate=f32-group+f64 lora=fused-epilogue(rank<=64)";
+    return "q4gemm-hip-gfx950 group=32 layout=n-major-lsb-nibble decode=gemv(m<=4; m=1,k<=4096: int4-digit dot8) "
+           "prefill=mfma-f32-16x16x4 accumulate=f32-group+f64 lora=fused-epilogue(rank<=64) "
+           "chain=fixed_shape_retained_hip_graph_replay";
 }
 
 const char* spaceslug_last_error(void) { return g_last_error.c_str(); }
@@ -445,6 +487,99 @@ int spaceslug_q4gemm_run(const spaceslug_q4_weight* weight, const float* x, floa
     } catch (...) {
         return fail(SPACESLUG_ERR_DEVICE, "spaceslug_q4gemm_run: unknown exception");
     }
+}
+
+spaceslug_q4_chain* spaceslug_q4_chain_create(const spaceslug_q4_step* steps, uint32_t count) {
+    if (!steps || count == 0) {
+        fail(SPACESLUG_ERR_INVALID, "spaceslug_q4_chain_create: need at least one step");
+        return nullptr;
+    }
+    for (uint32_t i = 0; i < count; ++i) {
+        const spaceslug_q4_step& s = steps[i];
+        if (const char* why = device_call_problem(s.d_x, s.d_w_packed, s.d_w_scales, s.d_lora_a, s.d_lora_b, s.d_y,
+                                                  s.m, s.n, s.k, s.rank)) {
+            fail(SPACESLUG_ERR_INVALID, "spaceslug_q4_chain_create: step " + std::to_string(i) + ": " + why);
+            return nullptr;
+        }
+    }
+    spaceslug_q4_chain* c = nullptr;
+    hipStream_t capture = nullptr;
+    bool capturing = false;
+    try {
+        DeviceState& dev = current_device();
+        c = new spaceslug_q4_chain;
+        check(hipGetDevice(&c->device), "hipGetDevice");
+        c->steps = count;
+        std::vector<spaceslug::Q4Plan> plans;
+        size_t ws = 0;
+        for (uint32_t i = 0; i < count; ++i) {
+            const spaceslug_q4_step& s = steps[i];
+            plans.push_back(spaceslug::plan_q4gemm(dev.info, s.m, s.n, s.k, s.d_lora_a ? s.rank : 0));
+            ws = std::max(ws, plans.back().workspace_bytes);
+        }
+        // The steps run one after another inside the graph, so one workspace serves all of them.
+        if (ws) check(hipMalloc(&c->workspace, ws), "hipMalloc (chain workspace)");
+        check(hipStreamCreateWithFlags(&capture, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+        check(hipStreamBeginCapture(capture, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+        capturing = true;
+        for (uint32_t i = 0; i < count; ++i) {
+            const spaceslug_q4_step& s = steps[i];
+            const bool lora = s.d_lora_a != nullptr;
+            check(spaceslug::launch_q4gemm(plans[i], dev.info, s.d_x, s.d_w_packed, s.d_w_scales, s.d_y, s.m, s.n, s.k,
+                                           s.d_lora_a, s.d_lora_b, lora ? s.rank : 0, lora ? s.lora_scale : 0.0f,
+                                           c->workspace, capture),
+                  "q4gemm launch (capture)");
+        }
+        capturing = false;
+        check(hipStreamEndCapture(capture, &c->graph), "hipStreamEndCapture");
+        check(hipGraphInstantiate(&c->exec, c->graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+        check(hipStreamDestroy(capture), "hipStreamDestroy");
+        capture = nullptr;
+        ok();
+        return c;
+    } catch (const HipError& e) {
+        from_hip(e);
+    } catch (const std::exception& e) {
+        fail(SPACESLUG_ERR_DEVICE, e.what());
+    } catch (...) {
+        fail(SPACESLUG_ERR_DEVICE, "spaceslug_q4_chain_create: unknown exception");
+    }
+    if (capturing) {
+        hipGraph_t partial = nullptr;
+        if (hipStreamEndCapture(capture, &partial) == hipSuccess && partial) (void)hipGraphDestroy(partial);
+    }
+    if (capture) (void)hipStreamDestroy(capture);
+    if (c) chain_release(c);
+    return nullptr;
+}
+
+int spaceslug_q4_chain_run(spaceslug_q4_chain* chain, void* stream) {
+    if (!chain) return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4_chain_run: null chain");
+    try {
+        int cur = -1;
+        check(hipGetDevice(&cur), "hipGetDevice");
+        if (cur != chain->device)
+            return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4_chain_run: chain lives on another device");
+        check(hipGraphLaunch(chain->exec, static_cast<hipStream_t>(stream)), "hipGraphLaunch");
+        return ok();
+    } catch (const HipError& e) {
+        return from_hip(e);
+    } catch (const std::exception& e) {
+        return fail(SPACESLUG_ERR_DEVICE, e.what());
+    } catch (...) {
+        return fail(SPACESLUG_ERR_DEVICE, "spaceslug_q4_chain_run: unknown exception");
+    }
+}
+
+void spaceslug_q4_chain_destroy(spaceslug_q4_chain* chain) {
+    if (!chain) return;
+    const int device = chain->device;
+    int prev = -1;
+    if (hipGetDevice(&prev) == hipSuccess && prev != device) (void)hipSetDevice(device);
+    // a replay still in flight reads the workspace: wait for the device first
+    (void)hipDeviceSynchronize();
+    chain_release(chain);
+    if (prev >= 0 && prev != device) (void)hipSetDevice(prev);
 }
 
 }  // extern "C"

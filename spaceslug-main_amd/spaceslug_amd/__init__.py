@@ -5,7 +5,8 @@ library with ctypes; BackendSession here does the same against
 libspaceslug_runtime.so (HIP kernels for gfx950 + the C-ABI declared in
 include/runtime_abi.h).
 """
-from .backend import BackendError, BackendSession, ExecutionResult, Q4Weight, library_path
+from .backend import BackendError, BackendSession, ExecutionResult, Q4Chain, Q4Step, Q4Weight, library_path
 from .parity import compare_float_arrays
 
-__all__ = ["BackendError", "BackendSession", "ExecutionResult", "Q4Weight", "compare_float_arrays", "library_path"]
+__all__ = ["BackendError", "BackendSession", "ExecutionResult", "Q4Chain", "Q4Step", "Q4Weight",
+           "compare_float_arrays", "library_path"]

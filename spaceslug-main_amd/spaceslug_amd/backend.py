@@ -122,6 +122,50 @@ class Q4Weight:
             pass
 
 
+class Q4Step(ctypes.Structure):
+    """spaceslug_q4_step (include/runtime_abi.h): one device-pointer projection of a chain."""
+
+    _fields_ = [("d_x", ctypes.c_void_p), ("d_w_packed", ctypes.c_void_p), ("d_w_scales", ctypes.c_void_p),
+                ("d_y", ctypes.c_void_p), ("m", ctypes.c_uint32), ("n", ctypes.c_uint32), ("k", ctypes.c_uint32),
+                ("d_lora_a", ctypes.c_void_p), ("d_lora_b", ctypes.c_void_p), ("rank", ctypes.c_uint32),
+                ("lora_scale", ctypes.c_float)]
+
+
+class Q4Chain:
+    """A retained chain of device-pointer projections replayed as one HIP graph
+    (spaceslug_q4_chain_create / _run / _destroy). The buffers named by the steps must
+    outlive the chain; refill their contents between runs, never move them."""
+
+    def __init__(self, session: "BackendSession", handle: int, steps: int) -> None:
+        self._session = session
+        self._handle = handle
+        self.steps = steps
+
+    def run(self, stream: int = 0) -> None:
+        if not self._handle:
+            raise BackendError("Q4Chain is closed")
+        lib = self._session._native()
+        self._session._check(lib.spaceslug_q4_chain_run(ctypes.c_void_p(self._handle), ctypes.c_void_p(stream)),
+                             "q4_chain_run")
+
+    def close(self) -> None:
+        if self._handle:
+            self._session._native().spaceslug_q4_chain_destroy(ctypes.c_void_p(self._handle))
+            self._handle = 0
+
+    def __enter__(self) -> "Q4Chain":
+        return self
+
+    def __exit__(self, *exc: Any) -> None:
+        self.close()
+
+    def __del__(self) -> None:  # best effort; explicit close() is preferred
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class BackendSession:
     """Runtime session bound to libspaceslug_runtime.so (HIP, gfx950)."""
 
@@ -178,6 +222,13 @@ class BackendSession:
             if hasattr(lib, "spaceslug_q4_quantize_device"):
                 lib.spaceslug_q4_quantize_device.argtypes = [ctypes.c_void_p] * 3 + [_u32, _u32, ctypes.c_void_p]
                 lib.spaceslug_q4_quantize_device.restype = ctypes.c_int
+            if hasattr(lib, "spaceslug_q4_chain_create"):
+                lib.spaceslug_q4_chain_create.argtypes = [ctypes.POINTER(Q4Step), _u32]
+                lib.spaceslug_q4_chain_create.restype = ctypes.c_void_p
+                lib.spaceslug_q4_chain_run.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+                lib.spaceslug_q4_chain_run.restype = ctypes.c_int
+                lib.spaceslug_q4_chain_destroy.argtypes = [ctypes.c_void_p]
+                lib.spaceslug_q4_chain_destroy.restype = None
             self._library = lib
         return self._library
 
@@ -317,6 +368,21 @@ class BackendSession:
                                                 ctypes.c_void_p(d_lora_b), ctypes.c_void_p(d_y), m, n, k, rank,
                                                 float(scale), ctypes.c_void_p(stream))
         self._check(code, "q4gemm_lora_device")
+
+    def create_q4_chain(self, steps: Sequence[dict[str, Any]]) -> Q4Chain:
+        """Records device-pointer projections into one replayable HIP graph. Each step is a dict with
+        d_x, d_w_packed, d_w_scales, d_y (device addresses), m, n, k and optionally d_lora_a, d_lora_b,
+        rank, lora_scale."""
+        lib = self._require("spaceslug_q4_chain_create")
+        arr = (Q4Step * max(1, len(steps)))()
+        for i, s in enumerate(steps):
+            arr[i] = Q4Step(s["d_x"], s["d_w_packed"], s["d_w_scales"], s["d_y"], s["m"], s["n"], s["k"],
+                            s.get("d_lora_a") or None, s.get("d_lora_b") or None, s.get("rank", 0),
+                            float(s.get("lora_scale", 0.0)))
+        handle = lib.spaceslug_q4_chain_create(arr, len(steps))
+        if not handle:
+            raise BackendError(f"native spaceslug_q4_chain_create failed: {self._last_error()}")
+        return Q4Chain(self, handle, len(steps))
 
     # -- fp32 -> int4 group-32 quantizer ----------------------------------------------------------
     def q4_quantize_values(self, w: Any, n: int, k: int) -> tuple[np.ndarray, np.ndarray]:

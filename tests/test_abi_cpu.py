@@ -41,7 +41,8 @@ def test_header_declares_the_expected_surface():
     for required in ("spaceslug_vector_add", "spaceslug_sgemm", "spaceslug_q4gemm", "spaceslug_q4gemm_lora",
                      "spaceslug_q4gemm_device", "spaceslug_q4gemm_lora_device", "spaceslug_q4_weight_create",
                      "spaceslug_q4_weight_destroy", "spaceslug_q4gemm_run", "spaceslug_q4gemm_capability",
-                     "spaceslug_last_error", "spaceslug_q4_quantize", "spaceslug_q4_quantize_device"):
+                     "spaceslug_last_error", "spaceslug_q4_quantize", "spaceslug_q4_quantize_device",
+                     "spaceslug_q4_chain_create", "spaceslug_q4_chain_run", "spaceslug_q4_chain_destroy"):
         assert required in names
 
 
@@ -144,6 +145,37 @@ def test_weight_handle_rejects_invalid_arguments(lib):
     assert lib.spaceslug_q4gemm_run(None, _p(x), _p(x), 1) == 1
 
 
+def test_chain_rejects_invalid_steps_before_device(lib):
+    from spaceslug_amd.backend import Q4Step
+
+    lib.spaceslug_q4_chain_create.restype = ctypes.c_void_p
+    lib.spaceslug_q4_chain_create.argtypes = [ctypes.POINTER(Q4Step), ctypes.c_uint32]
+    lib.spaceslug_q4_chain_run.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    lib.spaceslug_q4_chain_destroy.argtypes = [ctypes.c_void_p]
+    good = dict(d_x=0x100000, d_w_packed=0x200000, d_w_scales=0x300000, d_y=0x400000, m=1, n=8, k=64,
+                d_lora_a=None, d_lora_b=None, rank=0, lora_scale=0.0)
+
+    def steps(*variants):
+        arr = (Q4Step * len(variants))()
+        for i, v in enumerate(variants):
+            arr[i] = Q4Step(**{**good, **v})
+        return arr
+
+    assert lib.spaceslug_q4_chain_create(None, 1) is None
+    assert lib.spaceslug_q4_chain_create(steps({}), 0) is None
+    assert b"at least one step" in lib.spaceslug_last_error()
+    assert lib.spaceslug_q4_chain_create(steps({}, {"k": 48}), 2) is None
+    assert b"step 1" in lib.spaceslug_last_error() and b"k%32" in lib.spaceslug_last_error()
+    assert lib.spaceslug_q4_chain_create(steps({"d_x": 0x100004}), 1) is None
+    assert b"misaligned" in lib.spaceslug_last_error()
+    assert lib.spaceslug_q4_chain_create(steps({"d_lora_a": 0x500000}), 1) is None
+    assert b"both factors" in lib.spaceslug_last_error()
+    assert lib.spaceslug_q4_chain_create(steps({"d_lora_a": 0x500000, "d_lora_b": 0x600000, "rank": 65}), 1) is None
+    assert b"rank" in lib.spaceslug_last_error()
+    assert lib.spaceslug_q4_chain_run(None, None) == 1
+    lib.spaceslug_q4_chain_destroy(None)  # accepts NULL
+
+
 def _gpu_visible() -> bool:
     import torch
 
@@ -164,6 +196,13 @@ def test_no_cpu_fallback_without_device(lib):
     assert lib.spaceslug_sgemm(_p(a), _p(a), _p(a), 64, 64, 32, ctypes.byref(err)) == 2
     packed = np.zeros(64 * 32, np.uint8)
     assert lib.spaceslug_q4_quantize(_p(a), _p(packed, u8p), _p(a), 64, 64) == 2
+    from spaceslug_amd.backend import Q4Step
+
+    lib.spaceslug_q4_chain_create.restype = ctypes.c_void_p
+    lib.spaceslug_q4_chain_create.argtypes = [ctypes.POINTER(Q4Step), ctypes.c_uint32]
+    one = (Q4Step * 1)(Q4Step(0x100000, 0x200000, 0x300000, 0x400000, 1, 8, 64, None, None, 0, 0.0))
+    assert lib.spaceslug_q4_chain_create(one, 1) is None
+    assert b"no HIP device" in lib.spaceslug_last_error()
 
 
 # -- host shim (spaceslug_amd.BackendSession) --------------------------------------------------------
