@@ -33,3 +33,32 @@ def test_client_int4_call_on_gpu(runtime_lib_path, gpu, tmp_path):
     print(r.stdout, flush=True)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "q4gemm: PASS" in r.stdout
+
+
+CHAIN_SRC = REPO / "spaceslug-main_amd" / "examples" / "tiny_projection_chain.cpp"
+ROCM = Path("/opt/rocm")
+
+
+def build_chain_driver(runtime_lib_path: Path, out: Path) -> Path:
+    lib_dir = runtime_lib_path.parent
+    subprocess.run(["g++", "-std=c++17", "-O2", "-D__HIP_PLATFORM_AMD__", f"-I{REPO / 'include'}",
+                    f"-I{ROCM / 'include'}", str(CHAIN_SRC), f"-L{lib_dir}", "-lspaceslug_runtime",
+                    f"-L{ROCM / 'lib'}", "-lamdhip64", f"-Wl,-rpath,{lib_dir}", f"-Wl,-rpath,{ROCM / 'lib'}",
+                    "-o", str(out)], check=True)
+    return out
+
+
+def test_chain_driver_builds_and_skips_without_gpu(runtime_lib_path, tmp_path):
+    exe = build_chain_driver(runtime_lib_path, tmp_path / "chain")
+    r = subprocess.run([str(exe), "--allow-no-device"], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+
+
+@pytest.mark.gpu
+def test_chain_driver_on_gpu(runtime_lib_path, gpu, tmp_path):
+    exe = build_chain_driver(runtime_lib_path, tmp_path / "chain")
+    print("[gpu-case] C++ tiny projection chain", flush=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    print(r.stdout, flush=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert r.stdout.count("PASS") == 4
