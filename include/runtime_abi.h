@@ -180,6 +180,58 @@ int spaceslug_q4_chain_run(spaceslug_q4_chain* chain, void* stream);
 /* Waits for the chain's device, then releases the graph and the workspace. NULL is a no-op. */
 void spaceslug_q4_chain_destroy(spaceslug_q4_chain* chain);
 
+/* CQ4 codebook matmul (the reference's other quantized matmul, cactus_quant_matmul:
+ * vulkan-runtime/src/cactus/cactus_x86.cpp:133-240, 384-397; C bridge
+ * cactus_bridge_quant_matmul, cactus_x86_bridge.h). The struct has the field order of
+ * CactusQuantMatrixBridge, so a caller's bridge struct can be passed as is; fp16
+ * values are IEEE binary16 bit patterns in uint16_t. Per output:
+ *   C[m][n] = sum_g norm(n, g) * sum_k A'[m][g*gs + k] * codebook[idx(n, g, k)]
+ * where A' is the activation in the code basis: per group, A * input-scale
+ * reciprocal * left sign, normalized Walsh-Hadamard transform, * right sign, then
+ * gathered by the permutation (cactus_x86.cpp:87-113); with
+ * SPACESLUG_CQ4_FLAG_ORTHOGONAL, one group spans K and A' = (A * recip) x rotation
+ * (cactus_x86.cpp:197-210). Indices are LSB-first bit-packed per (row, group)
+ * (bits 1..4), or with SPACESLUG_CQ4_FLAG_INTERLEAVED_4ROW 4-bit 4-row panels with
+ * panel-major norms (cactus_x86.cpp:48-53, 151-159). Arithmetic is fp32 and C is
+ * rounded to fp16 once. Returns 1, writing nothing, where the reference returns
+ * without writing (null pointers, bits outside 1..4, zero sizes, K != gs * groups)
+ * and also for layouts it does not define: a Hadamard group size that is not a
+ * power of two up to 256 (its transform buffer holds 256), interleaved panels with
+ * bits != 4, N % 4 != 0 or gs % 8 != 0, and M > 65535. `expanded` and `norm_f32`
+ * are ignored, as the reference ignores them. */
+#define SPACESLUG_CQ4_FLAG_ORTHOGONAL (1u << 2)
+#define SPACESLUG_CQ4_FLAG_INTERLEAVED_4ROW (1u << 3)
+
+typedef struct spaceslug_cq4_matrix {
+    uint32_t bits;
+    uint32_t K;
+    uint32_t N;
+    uint32_t group_size;
+    uint32_t num_groups;
+    uint32_t flags;
+    const uint16_t* codebook;          /* fp16 [2^bits] */
+    const uint16_t* input_scale;       /* fp16 [K] or NULL */
+    const uint16_t* input_scale_recip; /* fp16 [K] or NULL (used first when both are set) */
+    const uint16_t* norms;             /* fp16 [N * groups] ([N] orthogonal), panel-major if interleaved */
+    const uint8_t* packed_indices;     /* N * groups * ceil(gs * bits / 8) bytes */
+    const int8_t* left_signs;          /* [gs] or NULL */
+    const int8_t* right_signs;         /* [gs] or NULL */
+    const uint32_t* permutation;       /* [gs] or NULL */
+    const uint16_t* rotation;          /* fp16 [K][K], orthogonal only */
+    const int8_t* expanded;            /* ignored */
+    const float* norm_f32;             /* ignored */
+} spaceslug_cq4_matrix;
+
+/* Synchronous host pointers: A is fp16 [M][K], C is fp16 [M][N]. */
+int spaceslug_cq4_matmul(const spaceslug_cq4_matrix* w, const uint16_t* a, uint32_t m, uint16_t* c);
+
+/* Device-pointer, stream-ordered variant: every array of `w` (the struct itself
+ * is host memory) and a, c are device pointers. The code-basis activations (M * K
+ * floats) live in the library-owned device workspace of spaceslug_q4gemm_device,
+ * ordered the same way across streams. */
+int spaceslug_cq4_matmul_device(const spaceslug_cq4_matrix* w, const uint16_t* d_a, uint32_t m, uint16_t* d_c,
+                                void* stream);
+
 #ifdef __cplusplus
 }
 #endif

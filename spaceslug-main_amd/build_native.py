@@ -22,7 +22,7 @@ OBJ_DIR = LIB_DIR / "obj"
 LIB_NAME = "libspaceslug_runtime.so"
 ARCH = "gfx950"
 
-SOURCES = ["q4_gemv.hip", "q4_gemm.hip", "q4_quantize.hip", "sgemm.hip", "runtime_abi.cpp"]
+SOURCES = ["q4_gemv.hip", "q4_gemm.hip", "q4_quantize.hip", "cq4.hip", "sgemm.hip", "runtime_abi.cpp"]
 
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}",

@@ -21,6 +21,7 @@
 #include <string>
 #include <vector>
 
+#include "cq4_kernels.hpp"
 #include "q4_kernels.hpp"
 
 namespace {
@@ -216,6 +217,42 @@ int run_device(const float* dx, const uint8_t* dw, const float* ds, const float*
     dev.ws_stream = st;
     dev.ws_used = true;
     return ok();
+}
+
+// -- CQ4 -------------------------------------------------------------------------------------------
+
+// Byte sizes of a CQ4 matrix's arrays (the counts cactus_x86.cpp reads), once its
+// shape has been accepted by cq4_problem.
+struct Cq4Sizes {
+    size_t codebook, scale, norms, packed, signs, perm, rotation;
+};
+
+bool pow2(uint32_t v) { return v && !(v & (v - 1)); }
+
+// Returns why the matrix/arguments are not accepted, or nullptr (see runtime_abi.h).
+const char* cq4_problem(const spaceslug_cq4_matrix* w, const void* a, uint32_t m, const void* c, Cq4Sizes* sz) {
+    if (!w || !a || !c) return "null pointer";
+    if (m == 0 || m > 65535) return "need 1 <= m <= 65535";
+    if (w->bits == 0 || w->bits > 4) return "bits must be 1..4";
+    if (w->K == 0 || w->N == 0 || w->group_size == 0 || w->num_groups == 0) return "zero dimension";
+    if (w->K > INT32_MAX || w->N > INT32_MAX) return "dimension too large";
+    if (!w->codebook || !w->norms || !w->packed_indices) return "codebook, norms and packed_indices are required";
+    const bool orth = (w->flags & SPACESLUG_CQ4_FLAG_ORTHOGONAL) != 0;
+    const bool inter = (w->flags & SPACESLUG_CQ4_FLAG_INTERLEAVED_4ROW) != 0;
+    if (orth && !w->rotation) return "the orthogonal mode needs a rotation";
+    if (!orth && (static_cast<uint64_t>(w->group_size) * w->num_groups != w->K)) return "K must equal group_size * num_groups";
+    if (!orth && (!pow2(w->group_size) || w->group_size > 256)) return "group_size must be a power of two <= 256";
+    const uint32_t gs = orth ? w->K : w->group_size, ng = orth ? 1 : w->num_groups;
+    if (inter && (w->bits != 4 || w->N % 4 || gs % 8)) return "interleaved panels need bits == 4, N % 4 == 0, gs % 8 == 0";
+    const size_t pgb = (static_cast<size_t>(gs) * w->bits + 7) / 8;
+    sz->codebook = (size_t{1} << w->bits) * 2;
+    sz->scale = static_cast<size_t>(w->K) * 2;
+    sz->norms = static_cast<size_t>(w->N) * ng * 2;
+    sz->packed = static_cast<size_t>(w->N) * ng * pgb;
+    sz->signs = orth ? 0 : gs;
+    sz->perm = orth ? 0 : static_cast<size_t>(gs) * 4;
+    sz->rotation = orth ? static_cast<size_t>(w->K) * w->K * 2 : 0;
+    return nullptr;
 }
 
 }  // namespace
@@ -486,6 +523,86 @@ int spaceslug_q4gemm_run(const spaceslug_q4_weight* weight, const float* x, floa
         return fail(SPACESLUG_ERR_DEVICE, e.what());
     } catch (...) {
         return fail(SPACESLUG_ERR_DEVICE, "spaceslug_q4gemm_run: unknown exception");
+    }
+}
+
+int spaceslug_cq4_matmul(const spaceslug_cq4_matrix* w, const uint16_t* a, uint32_t m, uint16_t* c) {
+    Cq4Sizes sz{};
+    if (const char* why = cq4_problem(w, a, m, c, &sz))
+        return fail(SPACESLUG_ERR_INVALID, std::string("spaceslug_cq4_matmul: ") + why);
+    const bool orth = (w->flags & SPACESLUG_CQ4_FLAG_ORTHOGONAL) != 0;
+    if (!orth && w->permutation)
+        for (uint32_t j = 0; j < w->group_size; ++j)
+            if (w->permutation[j] >= w->group_size)
+                return fail(SPACESLUG_ERR_INVALID, "spaceslug_cq4_matmul: permutation entry out of range");
+    try {
+        (void)current_device();
+        const size_t a_bytes = static_cast<size_t>(m) * w->K * 2, c_bytes = static_cast<size_t>(m) * w->N * 2;
+        const bool has_scale = w->input_scale_recip || w->input_scale;
+        StagingArena arena({a_bytes, c_bytes, static_cast<size_t>(m) * w->K * sizeof(float), sz.codebook,
+                            has_scale ? sz.scale : 0, sz.norms, sz.packed, w->left_signs ? sz.signs : 0,
+                            w->right_signs ? sz.signs : 0, w->permutation ? sz.perm : 0, sz.rotation});
+        auto up = [&](size_t slot, const void* host, size_t bytes) -> void* {
+            if (!host || !bytes) return nullptr;
+            void* d = arena.slice<void>(slot);
+            check(hipMemcpy(d, host, bytes, hipMemcpyHostToDevice), "hipMemcpy (cq4 input)");
+            return d;
+        };
+        spaceslug::Cq4View v{w->bits, w->K, w->N, w->group_size, w->num_groups, w->flags,
+                             static_cast<const uint16_t*>(up(3, w->codebook, sz.codebook)), nullptr, nullptr,
+                             static_cast<const uint16_t*>(up(5, w->norms, sz.norms)),
+                             static_cast<const uint8_t*>(up(6, w->packed_indices, sz.packed)),
+                             orth ? nullptr : static_cast<const int8_t*>(up(7, w->left_signs, sz.signs)),
+                             orth ? nullptr : static_cast<const int8_t*>(up(8, w->right_signs, sz.signs)),
+                             orth ? nullptr : static_cast<const uint32_t*>(up(9, w->permutation, sz.perm)),
+                             orth ? static_cast<const uint16_t*>(up(10, w->rotation, sz.rotation)) : nullptr};
+        if (w->input_scale_recip) v.input_scale_recip = static_cast<const uint16_t*>(up(4, w->input_scale_recip, sz.scale));
+        else if (w->input_scale) v.input_scale = static_cast<const uint16_t*>(up(4, w->input_scale, sz.scale));
+        const uint16_t* da = static_cast<const uint16_t*>(up(0, a, a_bytes));
+        check(spaceslug::launch_cq4_matmul(v, da, m, arena.slice<uint16_t>(1), arena.slice<float>(2), nullptr),
+              "cq4 launch");
+        check(hipMemcpy(c, arena.slice<uint16_t>(1), c_bytes, hipMemcpyDeviceToHost), "hipMemcpy (cq4 output)");
+        return ok();
+    } catch (const HipError& e) {
+        return from_hip(e);
+    } catch (const std::exception& e) {
+        return fail(SPACESLUG_ERR_DEVICE, e.what());
+    } catch (...) {
+        return fail(SPACESLUG_ERR_DEVICE, "spaceslug_cq4_matmul: unknown exception");
+    }
+}
+
+int spaceslug_cq4_matmul_device(const spaceslug_cq4_matrix* w, const uint16_t* d_a, uint32_t m, uint16_t* d_c,
+                                void* stream) {
+    Cq4Sizes sz{};
+    if (const char* why = cq4_problem(w, d_a, m, d_c, &sz))
+        return fail(SPACESLUG_ERR_INVALID, std::string("spaceslug_cq4_matmul_device: ") + why);
+    if (!aligned(d_a, 2) || !aligned(d_c, 2) || !aligned(w->packed_indices, 4) || !aligned(w->norms, 2) ||
+        !aligned(w->codebook, 2) || (w->permutation && !aligned(w->permutation, 4)))
+        return fail(SPACESLUG_ERR_INVALID, "spaceslug_cq4_matmul_device: misaligned device pointer");
+    const bool orth = (w->flags & SPACESLUG_CQ4_FLAG_ORTHOGONAL) != 0;
+    spaceslug::Cq4View v{w->bits, w->K, w->N, w->group_size, w->num_groups, w->flags, w->codebook,
+                         w->input_scale_recip ? nullptr : w->input_scale, w->input_scale_recip, w->norms,
+                         w->packed_indices, orth ? nullptr : w->left_signs, orth ? nullptr : w->right_signs,
+                         orth ? nullptr : w->permutation, orth ? w->rotation : nullptr};
+    try {
+        DeviceState& dev = current_device();
+        const hipStream_t st = static_cast<hipStream_t>(stream);
+        std::lock_guard<std::mutex> lock(g_device_mutex);
+        float* ws = static_cast<float*>(device_workspace(dev, static_cast<size_t>(m) * w->K * sizeof(float)));
+        if (!dev.ws_done) check(hipEventCreateWithFlags(&dev.ws_done, hipEventDisableTiming), "hipEventCreateWithFlags");
+        if (dev.ws_used && dev.ws_stream != st) check(hipStreamWaitEvent(st, dev.ws_done, 0), "hipStreamWaitEvent");
+        check(spaceslug::launch_cq4_matmul(v, d_a, m, d_c, ws, st), "cq4 launch");
+        check(hipEventRecord(dev.ws_done, st), "hipEventRecord");
+        dev.ws_stream = st;
+        dev.ws_used = true;
+        return ok();
+    } catch (const HipError& e) {
+        return from_hip(e);
+    } catch (const std::exception& e) {
+        return fail(SPACESLUG_ERR_DEVICE, e.what());
+    } catch (...) {
+        return fail(SPACESLUG_ERR_DEVICE, "spaceslug_cq4_matmul_device: unknown exception");
     }
 }
 

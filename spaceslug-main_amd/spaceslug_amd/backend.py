@@ -122,6 +122,23 @@ class Q4Weight:
             pass
 
 
+class CQ4MatrixStruct(ctypes.Structure):
+    """spaceslug_cq4_matrix (include/runtime_abi.h), the field order of the reference's
+    CactusQuantMatrixBridge (vulkan-runtime/src/cactus/cactus_x86_bridge.h)."""
+
+    _fields_ = [("bits", ctypes.c_uint32), ("K", ctypes.c_uint32), ("N", ctypes.c_uint32),
+                ("group_size", ctypes.c_uint32), ("num_groups", ctypes.c_uint32), ("flags", ctypes.c_uint32),
+                ("codebook", ctypes.c_void_p), ("input_scale", ctypes.c_void_p),
+                ("input_scale_recip", ctypes.c_void_p), ("norms", ctypes.c_void_p),
+                ("packed_indices", ctypes.c_void_p), ("left_signs", ctypes.c_void_p),
+                ("right_signs", ctypes.c_void_p), ("permutation", ctypes.c_void_p), ("rotation", ctypes.c_void_p),
+                ("expanded", ctypes.c_void_p), ("norm_f32", ctypes.c_void_p)]
+
+
+CQ4_FLAG_ORTHOGONAL = 1 << 2
+CQ4_FLAG_INTERLEAVED_4ROW = 1 << 3
+
+
 class Q4Step(ctypes.Structure):
     """spaceslug_q4_step (include/runtime_abi.h): one device-pointer projection of a chain."""
 
@@ -222,6 +239,12 @@ class BackendSession:
             if hasattr(lib, "spaceslug_q4_quantize_device"):
                 lib.spaceslug_q4_quantize_device.argtypes = [ctypes.c_void_p] * 3 + [_u32, _u32, ctypes.c_void_p]
                 lib.spaceslug_q4_quantize_device.restype = ctypes.c_int
+            if hasattr(lib, "spaceslug_cq4_matmul"):
+                lib.spaceslug_cq4_matmul.argtypes = [ctypes.c_void_p, ctypes.c_void_p, _u32, ctypes.c_void_p]
+                lib.spaceslug_cq4_matmul.restype = ctypes.c_int
+                lib.spaceslug_cq4_matmul_device.argtypes = [ctypes.c_void_p, ctypes.c_void_p, _u32, ctypes.c_void_p,
+                                                            ctypes.c_void_p]
+                lib.spaceslug_cq4_matmul_device.restype = ctypes.c_int
             if hasattr(lib, "spaceslug_q4_chain_create"):
                 lib.spaceslug_q4_chain_create.argtypes = [ctypes.POINTER(Q4Step), _u32]
                 lib.spaceslug_q4_chain_create.restype = ctypes.c_void_p
@@ -383,6 +406,41 @@ class BackendSession:
         if not handle:
             raise BackendError(f"native spaceslug_q4_chain_create failed: {self._last_error()}")
         return Q4Chain(self, handle, len(steps))
+
+    # -- CQ4 codebook matmul (cactus_quant_matmul) ---------------------------------------------------
+    def cq4_matmul_values(self, *, bits: int, K: int, N: int, group_size: int, num_groups: int, flags: int,
+                          codebook: Any, norms: Any, packed_indices: Any, a: Any, m: int,
+                          input_scale: Any = None, input_scale_recip: Any = None, left_signs: Any = None,
+                          right_signs: Any = None, permutation: Any = None, rotation: Any = None) -> np.ndarray:
+        """fp16 (uint16 bit patterns) C [m][N] = cactus_quant_matmul semantics, synchronous host arrays.
+        fp16 arrays are uint16 bit patterns; signs int8; permutation uint32; packed_indices uint8."""
+        lib = self._require("spaceslug_cq4_matmul")
+        keep = {}
+
+        def arr(x: Any, dtype: Any) -> int | None:
+            if x is None:
+                return None
+            v = np.ascontiguousarray(x, dtype=dtype)
+            keep[id(v)] = v
+            return v.ctypes.data
+
+        s = CQ4MatrixStruct(bits, K, N, group_size, num_groups, flags, arr(codebook, np.uint16),
+                            arr(input_scale, np.uint16), arr(input_scale_recip, np.uint16), arr(norms, np.uint16),
+                            arr(packed_indices, np.uint8), arr(left_signs, np.int8), arr(right_signs, np.int8),
+                            arr(permutation, np.uint32), arr(rotation, np.uint16), None, None)
+        aa = np.ascontiguousarray(a, dtype=np.uint16)
+        if m > 0 and aa.size != m * K:
+            raise BackendError(f"a must hold m*K = {m * K} fp16 values")
+        c = np.zeros((max(m, 1), N), np.uint16)
+        self._check(lib.spaceslug_cq4_matmul(ctypes.addressof(s), aa.ctypes.data, m, c.ctypes.data), "cq4_matmul")
+        return c
+
+    def cq4_matmul_device(self, matrix: CQ4MatrixStruct, d_a: int, m: int, d_c: int, stream: int = 0) -> None:
+        """`matrix` holds device addresses in its array fields."""
+        lib = self._require("spaceslug_cq4_matmul_device")
+        self._check(lib.spaceslug_cq4_matmul_device(ctypes.addressof(matrix), ctypes.c_void_p(d_a), m,
+                                                    ctypes.c_void_p(d_c), ctypes.c_void_p(stream)),
+                    "cq4_matmul_device")
 
     # -- fp32 -> int4 group-32 quantizer ----------------------------------------------------------
     def q4_quantize_values(self, w: Any, n: int, k: int) -> tuple[np.ndarray, np.ndarray]:

@@ -42,7 +42,8 @@ def test_header_declares_the_expected_surface():
                      "spaceslug_q4gemm_device", "spaceslug_q4gemm_lora_device", "spaceslug_q4_weight_create",
                      "spaceslug_q4_weight_destroy", "spaceslug_q4gemm_run", "spaceslug_q4gemm_capability",
                      "spaceslug_last_error", "spaceslug_q4_quantize", "spaceslug_q4_quantize_device",
-                     "spaceslug_q4_chain_create", "spaceslug_q4_chain_run", "spaceslug_q4_chain_destroy"):
+                     "spaceslug_q4_chain_create", "spaceslug_q4_chain_run", "spaceslug_q4_chain_destroy",
+                     "spaceslug_cq4_matmul", "spaceslug_cq4_matmul_device"):
         assert required in names
 
 
@@ -203,6 +204,15 @@ def test_no_cpu_fallback_without_device(lib):
     one = (Q4Step * 1)(Q4Step(0x100000, 0x200000, 0x300000, 0x400000, 1, 8, 64, None, None, 0, 0.0))
     assert lib.spaceslug_q4_chain_create(one, 1) is None
     assert b"no HIP device" in lib.spaceslug_last_error()
+    from oracle import cq4
+
+    W = cq4.random_matrix(np.random.default_rng(0), bits=4, K=64, N=8, group_size=64)
+    s = W.struct()
+    a16 = np.zeros((1, 64), np.uint16)
+    c16 = np.full((1, 8), 0x3C00, np.uint16)
+    lib.spaceslug_cq4_matmul.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p]
+    assert lib.spaceslug_cq4_matmul(ctypes.addressof(s), a16.ctypes.data, 1, c16.ctypes.data) == 2
+    assert np.all(c16 == 0x3C00)
 
 
 # -- host shim (spaceslug_amd.BackendSession) --------------------------------------------------------
