@@ -20,6 +20,7 @@ Also reported in the same JSON line:
     fp32 MFMA peak (the second half of the headline metric);
   - "small_batch" (M=16, K=N=4096, 32 weight copies per step) and "lora"
     (M=512, K=N=4096, rank 16) throughput;
+  - "cq4": the CQ4 codebook matmul on the reference's CQ4 benchmark shapes;
   - "cpu_baseline": the C CPU oracle (double-precision restatement of the
     reference's cpu_reference) on a bounded sample of the same GEMV workload,
     timed on this host's cores.
@@ -163,6 +164,39 @@ def bench_gemm(torch, session, m: int, n: int, k: int, copies: int, steps: int, 
             "tflops": tf, "gbs": by / per_call / 1e9, "flops_per_call": fl, "bytes_per_call": by,
             "roofline": {"bound": "mfma", "achieved": tf, "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": tf / FP32_MFMA_PEAK_TFLOPS}}
+
+
+def bench_cq4(torch, session, steps: int) -> dict:
+    """The CQ4 codebook matmul on the reference's CQ4 benchmark shapes (vulkan-runtime/bench/bench_cq4gemm.cpp:
+    bits 4, group 128, non-interleaved, input_scale_recip; 1024^3, 1x512x512, 1024x512x512), device-resident
+    inputs, one spaceslug_cq4_matmul_device call per step. TFLOP/s = 2*M*N*K / time, as the reference counts it
+    (transform and decode not counted)."""
+    from spaceslug_amd.backend import CQ4MatrixStruct
+
+    out = {}
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    for m, n, k in ((1024, 1024, 1024), (1, 512, 512), (1024, 512, 512)):
+        gs = 128
+        ng = k // gs
+        half = lambda *shape: (torch.rand(shape, generator=gen, device=dev) + 0.5).half()  # noqa: E731
+        codebook = (torch.rand(16, generator=gen, device=dev) * 2 - 1).half()
+        norms = half(n * ng)
+        recip = half(k)
+        packed = torch.randint(0, 256, (n * k // 2,), dtype=torch.uint8, device=dev, generator=gen)
+        a = (torch.rand((m, k), generator=gen, device=dev) * 2 - 1).half()
+        c = torch.empty((m, n), dtype=torch.float16, device=dev)
+        s = CQ4MatrixStruct(4, k, n, gs, ng, 0, codebook.data_ptr(), None, recip.data_ptr(), norms.data_ptr(),
+                            packed.data_ptr(), None, None, None, None, None, None)
+
+        def step():
+            session.cq4_matmul_device(s, a.data_ptr(), m, c.data_ptr(), torch.cuda.current_stream().cuda_stream)
+
+        reps = 20 if m > 1 else 200
+        ms = time_region(torch, lambda: [step() for _ in range(reps)], max(3, steps // 10), 2) / reps
+        out[f"{m}x{n}x{k}"] = {"us_per_call": round(ms * 1e3, 3),
+                               "tflops": round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 3)}
+    return out
 
 
 def copy_reference(torch, steps: int) -> dict:
@@ -309,6 +343,9 @@ def main() -> int:
         lo = bench_gemm(torch, session, 512, 4096, 4096, copies=1, steps=max(3, args.steps // 5), warmup=2, rank=16)
         result["lora"] = {"value": round(lo["tflops"], 3), "unit": "TFLOP/s",
                           "us_per_call": round(lo["ms_per_call"] * 1e3, 3), "roofline": lo["roofline"]}
+        torch.cuda.empty_cache()
+        print("[bench] cq4 codebook matmul", file=sys.stderr, flush=True)
+        result["cq4"] = bench_cq4(torch, session, args.steps)
     if args.cpu_seconds > 0:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
