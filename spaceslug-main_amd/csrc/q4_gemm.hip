@@ -350,10 +350,14 @@ __global__ __launch_bounds__(64) void lora_t_kernel(const float* __restrict__ x,
 // 128-bit load; the 4 lanes of a column read 64 contiguous bytes) and its
 // scale, then a 4 x 4 transpose across the 16-lane rows (v_permlane*_swap)
 // gives every lane word q of each of the 4 groups, the MFMA B layout. Two quads
-// are in flight while one computes (statically named buffers E and O).
-// Measured at M=16, K=N=4096: 16.4 us per call against 20.5 us for the split-K
-// kernel plus its reduction, and ~16 us for every other split tried.
-constexpr int kSkinnyWaves = 8;
+// are in flight while one computes (statically named buffers E and O); the
+// pipeline issues no load past the wavefront's last quad. KW is 16 when the
+// tile grid has no more workgroups than the chip has CUs (16 wavefronts per CU
+// from one tile), else 8. Measured at M=16, K=N=4096: 12.8 us per call (8
+// wavefronts: 14.2 us), against 20.5 us for the split-K kernel plus its
+// reduction.
+constexpr int kSkinnyWavesFew = 16;
+constexpr int kSkinnyWavesMany = 8;
 
 struct QuadOps {
     f32x4 alo[4], ahi[4];  // x[row j][32 g + 8 q .. +7] for the quad's 4 groups
@@ -415,15 +419,17 @@ __global__ __launch_bounds__(64 * KW) void q4_gemm_skinny_kernel(const float* x,
     const float* sq = ws + static_cast<size_t>(col) * G + q;
 
     double acc[4] = {0.0, 0.0, 0.0, 0.0};
-    if (qb < qe) {  // uniform per wavefront
+    if (qb < qe) {  // every condition below is uniform per wavefront
         QuadOps E, O;
         load_quad(E, arow, bq, sq, qb);
-        load_quad(O, arow, bq, sq, min(qb + 1, qe - 1));
+        if (qb + 1 < qe) load_quad(O, arow, bq, sq, qb + 1);
         for (int qi = qb; qi < qe; qi += 2) {
             mma_quad(E, acc);
-            load_quad(E, arow, bq, sq, min(qi + 2, qe - 1));  // past the end: a clamped reload, never used
-            if (qi + 1 < qe) mma_quad(O, acc);
-            load_quad(O, arow, bq, sq, min(qi + 3, qe - 1));
+            if (qi + 2 < qe) load_quad(E, arow, bq, sq, qi + 2);
+            if (qi + 1 < qe) {
+                mma_quad(O, acc);
+                if (qi + 3 < qe) load_quad(O, arow, bq, sq, qi + 3);
+            }
         }
     }
 
@@ -586,10 +592,17 @@ hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float*
     if (plan.kind == Q4Plan::kSkinny) {
         const int tiles_m = static_cast<int>((m + 15) / 16);
         const int tiles_n = static_cast<int>((n + 15) / 16);
-        hipLaunchKernelGGL((q4_gemm_skinny_kernel<kSkinnyWaves>), dim3(tiles_m * tiles_n), dim3(64 * kSkinnyWaves),
-                           0, stream, x, reinterpret_cast<const uint32_t*>(w_packed), w_scales, y,
-                           static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), tiles_m, tmat, lbp,
-                           static_cast<int>(rank), lora_scale);
+        const uint32_t* wq = reinterpret_cast<const uint32_t*>(w_packed);
+        if (tiles_m * tiles_n <= dev.cu_count)
+            hipLaunchKernelGGL((q4_gemm_skinny_kernel<kSkinnyWavesFew>), dim3(tiles_m * tiles_n),
+                               dim3(64 * kSkinnyWavesFew), 0, stream, x, wq, w_scales, y, static_cast<int>(m),
+                               static_cast<int>(n), static_cast<int>(k), tiles_m, tmat, lbp, static_cast<int>(rank),
+                               lora_scale);
+        else
+            hipLaunchKernelGGL((q4_gemm_skinny_kernel<kSkinnyWavesMany>), dim3(tiles_m * tiles_n),
+                               dim3(64 * kSkinnyWavesMany), 0, stream, x, wq, w_scales, y, static_cast<int>(m),
+                               static_cast<int>(n), static_cast<int>(k), tiles_m, tmat, lbp, static_cast<int>(rank),
+                               lora_scale);
         return hipGetLastError();
     }
     if (plan.kind == Q4Plan::kSkinnySplitK) {
