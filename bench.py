@@ -21,6 +21,8 @@ Also reported in the same JSON line:
   - "small_batch" (M=16, K=N=4096, 32 weight copies per step) and "lora"
     (M=512, K=N=4096, rank 16) throughput;
   - "cq4": the CQ4 codebook matmul on the reference's CQ4 benchmark shapes;
+  - "launch_floor": the per-launch time of a near-empty kernel replayed the same way, and the
+    fraction of the HBM peak that one launch of the GEMV's bytes could reach above it;
   - "cpu_baseline": the C CPU oracle (double-precision restatement of the
     reference's cpu_reference) on a bounded sample of the same GEMV workload,
     timed on this host's cores.
@@ -223,6 +225,31 @@ def copy_reference(torch, steps: int) -> dict:
     return out
 
 
+def launch_floor(torch, steps: int, bytes_per_launch: int) -> dict:
+    """Per-launch time of a kernel with almost no work (torch fill_ of one float), 64 launches captured
+    into one HIP graph and replayed like the GEMV sweep: the fixed cost every launch of the sweep pays
+    (completion, cache maintenance between dependent kernels, dispatch). With it, the highest fraction of
+    the HBM peak a single launch of `bytes_per_launch` bytes could reach is
+    bytes / (floor + bytes / peak) / peak."""
+    bufs = [torch.empty(1, dtype=torch.float32, device="cuda") for _ in range(64)]
+
+    def sweep():
+        for b in bufs:
+            b.fill_(1.0)
+
+    sweep()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        sweep()
+    ms = time_region(torch, g.replay, steps, 5)
+    del g
+    us = ms * 1e3 / len(bufs)
+    ideal_us = bytes_per_launch / (HBM_PEAK_GBS * 1e3)
+    return {"us_per_launch": round(us, 3), "kernel": "torch fill_ of 4 bytes, 64 launches replayed as one HIP graph",
+            "gemv_ceiling_frac": round(ideal_us / (us + ideal_us), 4)}
+
+
 def cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -351,6 +378,7 @@ def main() -> int:
     torch.cuda.empty_cache()
     print("[bench] copy reference", file=sys.stderr, flush=True)
     result["copy_reference"] = copy_reference(torch, args.steps)
+    result["launch_floor"] = launch_floor(torch, args.steps, result["roofline"]["bytes_per_launch"])
     if not args.gemv_only:
         print("[bench] prefill 2048x4096x14336", file=sys.stderr, flush=True)
         pre = bench_gemm(torch, session, 2048, 14336, 4096, copies=1, steps=max(3, args.steps // 10), warmup=2)

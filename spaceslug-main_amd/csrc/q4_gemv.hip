@@ -174,7 +174,7 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const float* x,  
     // derived from it in SGPRs. Every wavefront takes part in the barriers;
     // past-the-end wavefronts work on a clamped column and store nothing.
     const int wave =
-        __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)));
+        __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x * (kGemvThreads >> 6) + (threadIdx.x >> 6)));
     const int col0 = wave * CPW;
     const int G = K >> 5;
 
@@ -340,7 +340,7 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
     __shared__ float xcs[kGroups];
     const int lane = threadIdx.x & 63;
     const int wave =
-        __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)));
+        __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x * (kGemvThreads >> 6) + (threadIdx.x >> 6)));
     // Each wavefront streams one contiguous run of columns (a grid-strided
     // assignment, all wavefronts sweeping one band together, measured slower).
     const int cpb = D * iters;  // columns per wavefront (<= 64)
