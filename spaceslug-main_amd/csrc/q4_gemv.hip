@@ -231,8 +231,12 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const float* x,  
 // decoding to float (4 x (8 conversions + 1 shift + 8 fma)); the kernel is bound
 // by its per-wavefront VALU time as much as by HBM, so this is what buys speed.
 //
-// Each wavefront owns CPB = D * ITERS consecutive columns and keeps D columns of
-// loads in flight, computing column i while columns i+1 .. i+D stream in.
+// Each wavefront owns cpb = D + (D + 1) * reps consecutive columns in D + 1
+// register slots (column c in slot c % (D + 1)). Before computing column i it
+// issues the loads of column i + D into the slot column i - 1 has released, so
+// D columns stay in flight while a column computes (refilling a slot only after
+// computing it leaves D - 1 in flight during that time: measured 8.0 against
+// 7.5 us per launch at K = 4096, N = 14336).
 constexpr int kXDigits = 8;               // signed base-16 digits per recoded x value
 constexpr int kXFracBits = 30;            // |X| <= 2^30
 constexpr uint32_t kXBias = 0x88888888u;  // 8 in each of the eight digit positions
@@ -333,7 +337,8 @@ template <int SPC, int D>
 __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float* x,  // not restrict: see issue_chunk
                                                                    const u32x4* __restrict__ wq,
                                                                    const float* __restrict__ ws,
-                                                                   float* __restrict__ y, int N, int K, int iters) {
+                                                                   float* __restrict__ y, int N, int K, int reps) {
+    constexpr int S = D + 1;           // register slots
     constexpr int kGroups = 64 * SPC;  // groups per lane pass: K <= 32 * kGroups
     static_assert(kGroups * 2 == kGemvThreads, "x is recoded by two threads per group");
     __shared__ __align__(16) uint32_t xds[kGroups * 4 * kXDigits];
@@ -343,7 +348,7 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
         __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x * (kGemvThreads >> 6) + (threadIdx.x >> 6)));
     // Each wavefront streams one contiguous run of columns (a grid-strided
     // assignment, all wavefronts sweeping one band together, measured slower).
-    const int cpb = D * iters;  // columns per wavefront (<= 64)
+    const int cpb = D + S * reps;  // columns per wavefront (<= 64)
     const int col0 = wave * cpb;
     const int G = K >> 5;
 
@@ -363,7 +368,7 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
         off16[s] = static_cast<uint32_t>(64 * s + lane) * 16u;  // past K: beyond the buffer, reads 0
         off4[s] = static_cast<uint32_t>(64 * s + lane) * 4u;
     }
-    PipeSlot<SPC> slot[D];
+    PipeSlot<SPC> slot[S];
 #pragma unroll
     for (int d = 0; d < D; ++d) {
         pipe_issue<SPC>(slot[d], wq, ws, col0 + d, N, G, off16, off4);
@@ -421,25 +426,28 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
         xd.c[s] = xcs[gl];
     }
 
-    // Steady state: compute slot d (column i), then refill it with column i + D. (Reducing
-    // four columns at once with fewer instructions measured slower: the wavefront then
-    // waits out one long dependent chain per four columns.)
+    // Steady state, S columns per trip: issue column i + D into the free slot, then compute
+    // column i (slot i % S). The sched barriers keep each column's arithmetic between its
+    // own issue points: interleaved slots would make the wavefront wait for every
+    // outstanding load first. (Reducing four columns at once with fewer instructions
+    // measured slower: the wavefront then waits out one long dependent chain per four.)
     float result = 0.0f;
-    int i = 0;
-    for (int it = 0; it + 1 < iters; ++it) {
+    for (int r = 0; r < reps; ++r) {
 #pragma unroll
-        for (int d = 0; d < D; ++d, ++i) {
-            const float t = wave_reduce_dpp(pipe_partial<SPC>(slot[d], xd));
+        for (int s = 0; s < S; ++s) {
+            const int i = r * S + s;
+            pipe_issue<SPC>(slot[(s + D) % S], wq, ws, col0 + i + D, N, G, off16, off4);
+            __builtin_amdgcn_sched_barrier(0);
+            const float t = wave_reduce_dpp(pipe_partial<SPC>(slot[s], xd));
             result = lane == i ? t : result;
-            pipe_issue<SPC>(slot[d], wq, ws, col0 + i + D, N, G, off16, off4);
-            // Keep the next slot's arithmetic below this refill: otherwise the scheduler
-            // interleaves slots and must wait for every outstanding load first.
             __builtin_amdgcn_sched_barrier(0);
         }
     }
+    // The last D columns (slots 0 .. D-1, since reps * S is a multiple of S): no refills.
 #pragma unroll
-    for (int d = 0; d < D; ++d, ++i) {
-        const float t = wave_reduce_dpp(pipe_partial<SPC>(slot[d], xd));
+    for (int s = 0; s < D; ++s) {
+        const int i = reps * S + s;
+        const float t = wave_reduce_dpp(pipe_partial<SPC>(slot[s], xd));
         result = lane == i ? t : result;
     }
     // lane c holds column col0 + c: one coalesced store of the wavefront's run
@@ -471,22 +479,27 @@ hipError_t launch_rows(const float* x, const uint8_t* w_packed, const float* w_s
 
 }  // namespace
 
-// Single-row decode with K <= 4096: the pipelined kernel, D = 4 columns in flight
-// per wavefront and about 3.5 wavefronts per CU (measured best on MI355X for
-// K = 4096, N = 14336 among D in 1..8 and 896..14336 wavefronts).
+// Single-row decode with K <= 4096: the pipelined kernel with D = 4 columns in flight
+// per wavefront. Columns per wavefront: the fewest (cpb = 4 + 5 * reps, at most 64)
+// whose workgroups of 4 wavefronts all fit on the CUs at once, so no workgroup waits
+// for a second round. At K = 4096, N = 14336 that is 14 columns, 1024 wavefronts:
+// 7.48 us per launch, against 7.9-8.1 us for D = 2..5 at 15-19 columns, 8.3 us for
+// D = 1 and 9-10 us for all columns in flight at once; a grid 8% over one round
+// (276 workgroups) took 11.9 us. 7 columns at D = 3 (two wavefronts per SIMD)
+// measured the same within 1%.
 static hipError_t launch_gemv_pipelined(const DeviceInfo& dev, const float* x, const uint8_t* w_packed,
                                  const float* w_scales, float* y, uint32_t n, uint32_t k, hipStream_t stream) {
-    constexpr int D = 4;
-    const size_t target_waves = static_cast<size_t>(dev.cu_count) * 7 / 2;
-    size_t iters = (static_cast<size_t>(n) + target_waves * D - 1) / (target_waves * D);
-    if (iters < 1) iters = 1;
-    if (iters > 64 / D) iters = 64 / D;
-    const size_t cpb = D * iters;
+    constexpr int D = 4, S = D + 1, kMaxReps = (64 - D) / S;
+    const size_t waves_per_block = kGemvThreads / 64;
+    const size_t slots = static_cast<size_t>(dev.cu_count) * waves_per_block;  // wavefronts in one round
+    int reps = 0;
+    while (reps < kMaxReps && (static_cast<size_t>(n) + D + S * reps - 1) / (D + S * reps) > slots) ++reps;
+    const size_t cpb = D + S * reps;
     const size_t waves = (static_cast<size_t>(n) + cpb - 1) / cpb;
-    const size_t blocks = (waves + kGemvThreads / 64 - 1) / (kGemvThreads / 64);
+    const size_t blocks = (waves + waves_per_block - 1) / waves_per_block;
     hipLaunchKernelGGL((q4_gemv_pipe_kernel<2, D>), dim3(static_cast<unsigned>(blocks)), dim3(kGemvThreads), 0,
                        stream, x, reinterpret_cast<const u32x4*>(w_packed), w_scales, y, static_cast<int>(n),
-                       static_cast<int>(k), static_cast<int>(iters));
+                       static_cast<int>(k), reps);
     return hipGetLastError();
 }
 

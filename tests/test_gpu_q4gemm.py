@@ -93,6 +93,17 @@ def test_gemv_many_columns_per_wavefront(session, oracle, gpu):
     check(oracle, got, oracle.q4gemm_packed(c.x, c.packed, c.scales, threads=threads()), label="gemv many columns")
 
 
+@pytest.mark.parametrize("n", [4097, 9001, 14337, 30011, 65537])
+def test_gemv_one_row_column_runs(session, oracle, gpu, n):
+    """One row at K=4096 across the column counts where each wavefront's run of columns grows
+    (4, 9, 14, ... columns: N just past a multiple of the run, so the last wavefront is ragged)."""
+    m, k = 1, 4096
+    note(f"gemv m={m} n={n} k={k}")
+    c = make_case(m, n, k)
+    got = session.q4gemm_values(c.x, c.packed, c.scales, m, n, k)
+    check(oracle, got, oracle.q4gemm_packed(c.x, c.packed, c.scales, threads=threads()), label=f"gemv n={n}")
+
+
 @pytest.mark.parametrize("m,n,k", [(5, 1, 32), (5, 17, 96), (16, 256, 256), (17, 300, 1024), (32, 64, 64),
                                    (16, 4096, 4064), (9, 40, 128), (31, 33, 384),
                                    (33, 129, 160), (100, 300, 512), (130, 260, 1056), (256, 512, 2048)])
