@@ -353,29 +353,40 @@ __global__ __launch_bounds__(64) void lora_t_kernel(const float* __restrict__ x,
 // are in flight while one computes (statically named buffers E and O); the
 // pipeline issues no load past the wavefront's last quad. KW is 16 when the
 // tile grid has no more workgroups than the chip has CUs (16 wavefronts per CU
-// from one tile), else 8. Measured at M=16, K=N=4096: 12.8 us per call (8
-// wavefronts: 14.2 us), against 20.5 us for the split-K kernel plus its
-// reduction.
+// from one tile), else 8. Above 8 rows x reaches the MFMA through LDS (below).
+// Measured at M=16, K=N=4096: 10.9 us per call with x staged (12.5 us with x
+// loaded directly, 14.2 us with 8 wavefronts), against 20.5 us for the split-K
+// kernel plus its reduction.
 constexpr int kSkinnyWavesFew = 16;
 constexpr int kSkinnyWavesMany = 8;
+// Rows up to which x goes global -> VGPR directly; taller tiles copy it through LDS.
+constexpr int kSkinnyDirectMaxRows = 8;
 
-struct QuadOps {
-    f32x4 alo[4], ahi[4];  // x[row j][32 g + 8 q .. +7] for the quad's 4 groups
-    u32x4 bw;              // column j, group 4 * quad + q: its 16 packed bytes
-    float bs;              // scale of column j, group 4 * quad + q
+// Per-quad operands of one wavefront: x for the quad's 4 groups (in registers
+// straight from global memory, or copied through LDS first, below) and the
+// weights and scales of its column.
+struct QuadW {
+    u32x4 bw;  // column j, group 4 * quad + q: its 16 packed bytes
+    float bs;  // scale of column j, group 4 * quad + q
 };
 
-__device__ __forceinline__ void load_quad(QuadOps& o, const float* arow, const u32x4* bq, const float* sq, int qi) {
-#pragma unroll
-    for (int gi = 0; gi < 4; ++gi) {
-        o.alo[gi] = *reinterpret_cast<const f32x4*>(arow + (4 * qi + gi) * 32);
-        o.ahi[gi] = *reinterpret_cast<const f32x4*>(arow + (4 * qi + gi) * 32 + 4);
-    }
+__device__ __forceinline__ void load_quad_w(QuadW& o, const u32x4* bq, const float* sq, int qi) {
     o.bw = __builtin_nontemporal_load(bq + 4 * qi);
     o.bs = __builtin_nontemporal_load(sq + 4 * qi);
 }
 
-__device__ __forceinline__ void mma_quad(const QuadOps& o, double (&acc)[4]) {
+// x[row j][32 g + 8 q .. +7] for the quad's 4 groups: two 128-bit loads per group, each
+// instruction touching half of 16 rows' 128-byte lines.
+__device__ __forceinline__ void load_quad_x(f32x4 (&alo)[4], f32x4 (&ahi)[4], const float* arow, int qi) {
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) {
+        alo[gi] = *reinterpret_cast<const f32x4*>(arow + (4 * qi + gi) * 32);
+        ahi[gi] = *reinterpret_cast<const f32x4*>(arow + (4 * qi + gi) * 32 + 4);
+    }
+}
+
+__device__ __forceinline__ void mma_quad(const QuadW& o, const f32x4 (&alo)[4], const f32x4 (&ahi)[4],
+                                         double (&acc)[4]) {
     const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
     const u32x4 bw = transpose_rows(o.bw);  // word q of each of the quad's groups
     const f32x4 bs = gather_rows(o.bs);     // the quad's 4 scales of column j
@@ -386,7 +397,7 @@ __device__ __forceinline__ void mma_quad(const QuadOps& o, double (&acc)[4]) {
         f32x4 P;
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            const float av = t < 4 ? o.alo[gi][t & 3] : o.ahi[gi][t & 3];
+            const float av = t < 4 ? alo[gi][t & 3] : ahi[gi][t & 3];
             P = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[t], t == 0 ? zero : P, 0, 0, 0);
         }
         const double sc = static_cast<double>(bs[gi]) * kSixteenthsUnit;
@@ -395,14 +406,29 @@ __device__ __forceinline__ void mma_quad(const QuadOps& o, double (&acc)[4]) {
     }
 }
 
-template <int KW>
+// With kStageX, each wavefront copies its quad of x (16 rows x 128 floats, 8 KiB)
+// global -> LDS by global_load_lds_dwordx4, two full 512-byte row runs per
+// instruction, and reads its MFMA operands from there: the register-direct loads
+// above touch twice the cache lines for the same bytes, which at 16 rows (x read
+// whole by every CU) cost 13% of the kernel (M=16, K=N=4096: 12.5 -> 10.9 us).
+// Row j's 16-byte chunk c (k = 4 c .. 4 c + 3 of the quad) sits at chunk c ^ j of
+// the row, so a pass of 16 lanes reading one chunk of each row hits 16 distinct
+// bank groups. The next quad's copy starts once this quad's operands are in
+// registers. At M <= 8 the copy moves rows the tile does not use and the direct
+// loads are faster (M=5: 9.9 against 10.7 us).
+constexpr int kQuadXFloats = 16 * 128;
+
+template <int KW, bool kStageX>
 // x, wq and ws are not __restrict__ for the reason given at q4_gemm_mfma_kernel.
 __global__ __launch_bounds__(64 * KW) void q4_gemm_skinny_kernel(const float* x, const uint32_t* wq, const float* ws,
                                                                 float* __restrict__ y, int M, int N, int K,
                                                                 int tiles_m, const float* __restrict__ tmat,
                                                                 const float* __restrict__ lb, int R, float lscale) {
+    // Per wavefront: its x unit (staged form), then 256 partial sums in double.
+    constexpr int kRegionFloats = kStageX ? kQuadXFloats : 512;
+    __shared__ f32x4 smem[KW * kRegionFloats / 4];
     const int lane = threadIdx.x & 63;
-    const int wk = threadIdx.x >> 6;
+    const int wk = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int j = lane & 15;
     const int q = lane >> 4;
     const int G = K >> 5;
@@ -412,30 +438,68 @@ __global__ __launch_bounds__(64 * KW) void q4_gemm_skinny_kernel(const float* x,
     const int qpw = (Q + KW - 1) / KW;
     const int qb = wk * qpw;
     const int qe = min(Q, qb + qpw);
-    const int row = min(m0 + j, M - 1);
     const int col = min(n0 + j, N - 1);
-    const float* arow = x + static_cast<size_t>(row) * K + 8 * q;
     const u32x4* bq = reinterpret_cast<const u32x4*>(wq + static_cast<size_t>(col) * (K >> 3)) + q;
     const float* sq = ws + static_cast<size_t>(col) * G + q;
+    const float* arow = x + static_cast<size_t>(min(m0 + j, M - 1)) * K + 8 * q;
+    float* xs = reinterpret_cast<float*>(smem) + wk * kRegionFloats;
+
+    // Staged copy: instruction i moves rows 2i and 2i+1; lane l fetches the chunk that
+    // lands at position l & 31 of row 2i + (l >> 5).
+    const float* xsrc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int r = 2 * i + (lane >> 5);
+        xsrc[i] = x + static_cast<size_t>(min(m0 + r, M - 1)) * K + 4 * ((lane & 31) ^ r);
+    }
+    auto issue_x = [&](int qi) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) __builtin_amdgcn_global_load_lds(xsrc[i] + qi * 128, xs + i * 256, 16, 0, 0);
+    };
+    auto stage_start = [&](int qi) {
+        if constexpr (kStageX) issue_x(qi);
+    };
+    // One quad: its x operands (staged: wait for the copy, read LDS, start the next copy
+    // into the same bytes), then the MFMAs.
+    auto step = [&](const QuadW& w, int qi, double (&acc)[4]) {
+        f32x4 alo[4], ahi[4];
+        if constexpr (kStageX) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int gi = 0; gi < 4; ++gi) {
+                alo[gi] = *reinterpret_cast<const f32x4*>(xs + j * 128 + (((8 * gi + 2 * q) ^ j) << 2));
+                ahi[gi] = *reinterpret_cast<const f32x4*>(xs + j * 128 + (((8 * gi + 2 * q + 1) ^ j) << 2));
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (qi + 1 < qe) issue_x(qi + 1);  // uniform
+        } else {
+            load_quad_x(alo, ahi, arow, qi);
+        }
+        mma_quad(w, alo, ahi, acc);
+    };
 
     double acc[4] = {0.0, 0.0, 0.0, 0.0};
     if (qb < qe) {  // every condition below is uniform per wavefront
-        QuadOps E, O;
-        load_quad(E, arow, bq, sq, qb);
-        if (qb + 1 < qe) load_quad(O, arow, bq, sq, qb + 1);
+        QuadW E, O;
+        stage_start(qb);
+        load_quad_w(E, bq, sq, qb);
+        if (qb + 1 < qe) load_quad_w(O, bq, sq, qb + 1);
         for (int qi = qb; qi < qe; qi += 2) {
-            mma_quad(E, acc);
-            if (qi + 2 < qe) load_quad(E, arow, bq, sq, qi + 2);
+            step(E, qi, acc);
+            if (qi + 2 < qe) load_quad_w(E, bq, sq, qi + 2);
             if (qi + 1 < qe) {
-                mma_quad(O, acc);
-                if (qi + 3 < qe) load_quad(O, arow, bq, sq, qi + 3);
+                step(O, qi + 1, acc);
+                if (qi + 3 < qe) load_quad_w(O, bq, sq, qi + 3);
             }
         }
     }
 
-    __shared__ double red[KW][256];
+    // Partial sums through the wavefront's own LDS region (no copy is in flight any
+    // more), summed in wavefront order.
+    double* red = reinterpret_cast<double*>(smem);
+    constexpr int kRedStride = kRegionFloats / 2;  // doubles per wavefront region
 #pragma unroll
-    for (int r = 0; r < 4; ++r) red[wk][(4 * q + r) * 16 + j] = acc[r];
+    for (int r = 0; r < 4; ++r) red[wk * kRedStride + (4 * q + r) * 16 + j] = acc[r];
     __syncthreads();
     for (int e = threadIdx.x; e < 256; e += 64 * KW) {
         const int rr = m0 + (e >> 4);
@@ -443,7 +507,7 @@ __global__ __launch_bounds__(64 * KW) void q4_gemm_skinny_kernel(const float* x,
         if (rr >= M || cc >= N) continue;
         double s = 0.0;
 #pragma unroll
-        for (int w = 0; w < KW; ++w) s += red[w][e];
+        for (int w = 0; w < KW; ++w) s += red[w * kRedStride + e];
         if (lb != nullptr) {
             double t = 0.0;
             for (int r = 0; r < R; ++r)
@@ -593,16 +657,16 @@ hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float*
         const int tiles_m = static_cast<int>((m + 15) / 16);
         const int tiles_n = static_cast<int>((n + 15) / 16);
         const uint32_t* wq = reinterpret_cast<const uint32_t*>(w_packed);
-        if (tiles_m * tiles_n <= dev.cu_count)
-            hipLaunchKernelGGL((q4_gemm_skinny_kernel<kSkinnyWavesFew>), dim3(tiles_m * tiles_n),
-                               dim3(64 * kSkinnyWavesFew), 0, stream, x, wq, w_scales, y, static_cast<int>(m),
-                               static_cast<int>(n), static_cast<int>(k), tiles_m, tmat, lbp, static_cast<int>(rank),
-                               lora_scale);
-        else
-            hipLaunchKernelGGL((q4_gemm_skinny_kernel<kSkinnyWavesMany>), dim3(tiles_m * tiles_n),
-                               dim3(64 * kSkinnyWavesMany), 0, stream, x, wq, w_scales, y, static_cast<int>(m),
-                               static_cast<int>(n), static_cast<int>(k), tiles_m, tmat, lbp, static_cast<int>(rank),
-                               lora_scale);
+        const bool few = tiles_m * tiles_n <= dev.cu_count;
+        const bool stage = m > kSkinnyDirectMaxRows;
+        const int waves = few ? kSkinnyWavesFew : kSkinnyWavesMany;
+        auto kernel = few ? (stage ? q4_gemm_skinny_kernel<kSkinnyWavesFew, true>
+                                   : q4_gemm_skinny_kernel<kSkinnyWavesFew, false>)
+                          : (stage ? q4_gemm_skinny_kernel<kSkinnyWavesMany, true>
+                                   : q4_gemm_skinny_kernel<kSkinnyWavesMany, false>);
+        hipLaunchKernelGGL(kernel, dim3(tiles_m * tiles_n), dim3(64 * waves), 0, stream, x, wq, w_scales, y,
+                           static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), tiles_m, tmat, lbp,
+                           static_cast<int>(rank), lora_scale);
         return hipGetLastError();
     }
     if (plan.kind == Q4Plan::kSkinnySplitK) {

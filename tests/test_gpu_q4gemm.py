@@ -104,6 +104,17 @@ def test_gemv_one_row_column_runs(session, oracle, gpu, n):
     check(oracle, got, oracle.q4gemm_packed(c.x, c.packed, c.scales, threads=threads()), label=f"gemv n={n}")
 
 
+@pytest.mark.parametrize("m,n,k", [(8, 5000, 512), (9, 4096, 512), (24, 700, 2048), (32, 4096, 1024), (31, 1000, 640)])
+def test_small_m_both_x_paths(session, oracle, gpu, m, n, k):
+    """M <= 32 with K % 128 == 0: x loaded straight into registers (M <= 8) or copied through
+    LDS first (M > 8), each with 16 wavefronts per tile (tile grid fits the CUs) and with 8
+    (it does not: 8x5000, 32x4096), on ragged row tiles (24, 31) and K of 4 to 16 quads."""
+    note(f"small-m m={m} n={n} k={k}")
+    c = make_case(m, n, k)
+    got = session.q4gemm_values(c.x, c.packed, c.scales, m, n, k)
+    check(oracle, got, oracle.q4gemm_packed(c.x, c.packed, c.scales, threads=threads()), label=f"small-m {m}x{n}x{k}")
+
+
 @pytest.mark.parametrize("m,n,k", [(5, 1, 32), (5, 17, 96), (16, 256, 256), (17, 300, 1024), (32, 64, 64),
                                    (16, 4096, 4064), (9, 40, 128), (31, 33, 384),
                                    (33, 129, 160), (100, 300, 512), (130, 260, 1056), (256, 512, 2048)])
