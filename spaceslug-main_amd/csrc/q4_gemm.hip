@@ -1,25 +1,22 @@
 // fp32-MFMA int4 GEMM for 5+ rows (prefill, small-batch decode, LoRA projections).
-// Two kernels: q4_gemm_skinny_kernel for M <= 32 with K % 128 == 0 (described
-// at its definition) and q4_gemm_mfma_kernel for everything else, described here.
+// Three kernels: q4_gemm_wide_kernel for M > 32, q4_gemm_skinny_kernel for
+// M <= 32 with K % 128 == 0 and q4_gemm_mfma_kernel (K-split) for the other
+// M <= 32 shapes, each described at its definition.
 //
 // Replaces q4gemm.comp:61-175 (64x64 tile, LDS-staged dequantised B, 4x4 FMA
-// micro-tile per thread) with a CDNA4 design built on v_mfma_f32_16x16x4_f32:
-//   - a wavefront owns a (16*WM) x (16*WN) output block, WM x WN MFMA tiles;
+// micro-tile per thread) with a CDNA4 design built on v_mfma_f32_16x16x4_f32.
+// Common to all three:
 //   - per 32-value scale group, lane (j = l%16, q = l/16) feeds the MFMA K slot
 //     q with k = 8q + t at step t = 0..7, so its B operands for column j are
 //     the 8 nibbles of ONE 32-bit word of the packed column (word q of the
-//     group's 16 bytes) and its A operands are 8 consecutive floats of row j
-//     (two 128-bit loads). Weights are decoded in registers to v / 16
-//     (v_cvt_off_f32_i4, exact; the factor 16 joins the scale) straight into
-//     the MFMA operand;
+//     group's 16 bytes) and its A operands are 8 consecutive floats of row j.
+//     Weights are decoded to v / 16 (v_cvt_off_f32_i4, exact; the factor 16
+//     joins the scale);
 //   - the MFMA accumulates P = x * v over one group (8 steps) in fp32 from
 //     zero, and the group is folded into a float64 accumulator as
 //     acc += (double)s * P. Scale application moves out of the inner loop, and
 //     the long K sum is carried in double, which keeps the max relative error
 //     against the double-precision reference well under 1e-5 at K = 4096;
-//   - operands of the next PD groups are in flight while a group computes (a
-//     ring of register buffers); A rows and weight columns go global -> VGPR
-//     through L1/L2 with no LDS round trip;
 //   - large grids are XCD-aware: workgroup ids are remapped so each of the 8
 //     XCDs (one L2 each) walks a contiguous band of output tiles, sharing A
 //     rows and weight columns within its L2;
@@ -84,6 +81,10 @@ __device__ __forceinline__ void load_group(GroupOps<WM, WN>& o, const float* con
     }
 }
 
+// K-split kernel for the small-M shapes the skinny kernel does not take
+// (M <= 32, K % 128 != 0): a wavefront owns a (16*WM) x (16*WN) output block,
+// its A operands (two 128-bit loads of row j per group) and weight words go
+// global -> VGPR, and PD groups are in flight behind the one being computed.
 template <int WM, int WN, int WAVES_M, int WAVES_N, int PD>
 // x, wq and ws are deliberately not __restrict__: as provably invariant loads
 // the compiler would be free to re-issue the prefetched group's loads at their
@@ -158,96 +159,27 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void q4_gemm_mfma_kernel(
         }
     };
     if (g_begin < g_end) {
-        if constexpr (PD == 1) {
-            // Double buffer in plain register arrays: issue group g+1 into the *_n
-            // registers, compute group g, then take them over (with 16*WM*WN MFMAs
-            // per group the loads have landed by then).
-            f32x4 alo[WM], ahi[WM];
-            uint32_t bw[WN];
-            float bs[WN];
+        // PD + 1 buffers used in rotation: while buffer s computes group g+s,
+        // buffer (s+PD) % (PD+1) receives group g+s+PD, so PD groups are in flight
+        // behind the one being computed. The rotation is unrolled, so no buffer
+        // is copied (a register copy would wait for its loads). Loads past the
+        // split are clamped to its last group and never accumulated.
+        constexpr int NB = PD + 1;
+        GroupOps<WM, WN> buf[NB];
 #pragma unroll
-            for (int tm = 0; tm < WM; ++tm) {
-                alo[tm] = *reinterpret_cast<const f32x4*>(arow[tm] + g_begin * 32);
-                ahi[tm] = *reinterpret_cast<const f32x4*>(arow[tm] + g_begin * 32 + 4);
-            }
+        for (int p = 0; p < PD; ++p) {
+            load_group<WM, WN>(buf[p], arow, bcol, scol, min(g_begin + p, g_end - 1));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        for (int g = g_begin; g < g_end; g += NB) {
 #pragma unroll
-            for (int tn = 0; tn < WN; ++tn) {
-                bw[tn] = bcol[tn][g_begin * 4];
-                bs[tn] = scol[tn][g_begin];
-            }
-            for (int g = g_begin; g < g_end; ++g) {
-                const int gn = min(g + 1, g_end - 1);
-                f32x4 alo_n[WM], ahi_n[WM];
-                uint32_t bw_n[WN];
-                float bs_n[WN];
-#pragma unroll
-                for (int tm = 0; tm < WM; ++tm) {
-                    alo_n[tm] = *reinterpret_cast<const f32x4*>(arow[tm] + gn * 32);
-                    ahi_n[tm] = *reinterpret_cast<const f32x4*>(arow[tm] + gn * 32 + 4);
-                }
-#pragma unroll
-                for (int tn = 0; tn < WN; ++tn) {
-                    bw_n[tn] = bcol[tn][gn * 4];
-                    bs_n[tn] = scol[tn][gn];
-                }
-                f32x4 P[WM][WN];
-                float bv[WN][8];
-#pragma unroll
-                for (int tn = 0; tn < WN; ++tn) nibbles_signed_16th_mfma(bw[tn], bv[tn]);
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-#pragma unroll
-                    for (int tm = 0; tm < WM; ++tm) {
-                        const float av = t < 4 ? alo[tm][t & 3] : ahi[tm][t & 3];
-#pragma unroll
-                        for (int tn = 0; tn < WN; ++tn)
-                            P[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[tn][t], t == 0 ? zero : P[tm][tn],
-                                                                             0, 0, 0);
-                    }
-                }
-#pragma unroll
-                for (int tn = 0; tn < WN; ++tn) {
-                    const double sc = static_cast<double>(bs[tn]) * kSixteenthsUnit;
-#pragma unroll
-                    for (int tm = 0; tm < WM; ++tm)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i)
-                            acc[tm][tn][i] = fma(sc, static_cast<double>(P[tm][tn][i]), acc[tm][tn][i]);
-                }
-#pragma unroll
-                for (int tm = 0; tm < WM; ++tm) {
-                    alo[tm] = alo_n[tm];
-                    ahi[tm] = ahi_n[tm];
-                }
-#pragma unroll
-                for (int tn = 0; tn < WN; ++tn) {
-                    bw[tn] = bw_n[tn];
-                    bs[tn] = bs_n[tn];
-                }
-            }
-        } else {
-            // PD + 1 buffers used in rotation: while buffer s computes group g+s,
-            // buffer (s+PD) % (PD+1) receives group g+s+PD, so PD groups are in flight
-            // behind the one being computed. The rotation is unrolled, so no buffer
-            // is copied (a register copy would wait for its loads). Loads past the
-            // split are clamped to its last group and never accumulated.
-            constexpr int NB = PD + 1;
-            GroupOps<WM, WN> buf[NB];
-#pragma unroll
-            for (int p = 0; p < PD; ++p) {
-                load_group<WM, WN>(buf[p], arow, bcol, scol, min(g_begin + p, g_end - 1));
+            for (int sl = 0; sl < NB; ++sl) {
+                load_group<WM, WN>(buf[(sl + PD) % NB], arow, bcol, scol, min(g + sl + PD, g_end - 1));
                 __builtin_amdgcn_sched_barrier(0);
-            }
-            for (int g = g_begin; g < g_end; g += NB) {
-#pragma unroll
-                for (int sl = 0; sl < NB; ++sl) {
-                    load_group<WM, WN>(buf[(sl + PD) % NB], arow, bcol, scol, min(g + sl + PD, g_end - 1));
-                    __builtin_amdgcn_sched_barrier(0);
-                    if (g + sl < g_end) do_group(buf[sl]);  // uniform across the workgroup
-                    // keep the next slot's loads and work below this point so each slot
-                    // waits only for its own loads
-                    __builtin_amdgcn_sched_barrier(0);
-                }
+                if (g + sl < g_end) do_group(buf[sl]);  // uniform across the workgroup
+                // keep the next slot's loads and work below this point so each slot
+                // waits only for its own loads
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
     }
@@ -255,6 +187,218 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void q4_gemm_mfma_kernel(
     if (lb != nullptr && blockIdx.y == 0) {
         // LoRA epilogue: + lscale * T[m0.., :R] * lb[:R, n0..] on the MFMA, r in the K slot
         // (T = x * la, M x R, summed by lora_t_reduce_kernel).
+#pragma unroll
+        for (int tm = 0; tm < WM; ++tm) {
+            const int row = min(m0 + 16 * tm + j, M - 1);
+#pragma unroll
+            for (int tn = 0; tn < WN; ++tn) {
+                const int col = min(n0 + 16 * tn + j, N - 1);
+                f32x4 P = zero;
+                for (int r0 = 0; r0 < R; r0 += 4) {
+                    const int r = r0 + q;
+                    const float av = r < R ? tmat[static_cast<size_t>(row) * R + r] : 0.0f;
+                    const float bv = r < R ? lb[static_cast<size_t>(r) * N + col] : 0.0f;
+                    P = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, P, 0, 0, 0);
+                }
+                const double s = static_cast<double>(lscale);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[tm][tn][i] = fma(s, static_cast<double>(P[i]), acc[tm][tn][i]);
+            }
+        }
+    }
+
+    float* dst = out + static_cast<size_t>(blockIdx.y) * M * N;
+#pragma unroll
+    for (int tm = 0; tm < WM; ++tm) {
+#pragma unroll
+        for (int tn = 0; tn < WN; ++tn) {
+            const int col = n0 + 16 * tn + j;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = m0 + 16 * tm + 4 * q + i;
+                if (row < M && col < N) dst[static_cast<size_t>(row) * N + col] = static_cast<float>(acc[tm][tn][i]);
+            }
+        }
+    }
+}
+
+// Wide tile for M > 32 (prefill, LoRA projections): 128 x 128 outputs per
+// workgroup, 2 x 2 wavefronts of 64 x 64 (4 x 4 MFMA tiles each), one wavefront
+// per SIMD (444 registers). Per 32-value group the workgroup stages, in one of
+// two LDS buffers:
+//   - the A tile (128 rows x 32 floats, 16 KiB), copied global -> LDS by
+//     global_load_lds_dwordx4 (no VGPRs): 16 copies of 8 full 128-byte rows,
+//     four per wavefront. Row chunks are XOR-swizzled so that the 16 rows a
+//     pass of MFMA-operand reads touches fall on 16 distinct bank groups;
+//   - the dequantised B tile (128 columns x 32 values as v/16 floats, 16 KiB):
+//     each thread loads 8 packed bytes (two words of one column), decodes them
+//     once for the whole workgroup, and writes them in the MFMA B layout, so
+//     every wavefront reads its B operands as linear 1 KiB runs.
+// Group g+1 is staged while group g computes; one barrier per group. Against
+// the same tile with operands loaded global -> VGPR by each wavefront (every A
+// row read by both N-wavefronts, each load instruction touching half of 16
+// rows' lines, every B word decoded by both M-wavefronts): 2.34 against
+// 2.41 ms at M=2048, K=4096, N=14336.
+struct WideLdsStage {
+    // A tile, 128 rows x 32 floats: row r's 16-byte chunk c (k = 32 g + 4 c .. +3) at
+    // f32x4 index (r >> 1) * 16 + 8 * (r & 1) + (c ^ ((r >> 1) & 7)).
+    f32x4 a[16][64];
+    // B tile, v/16 floats in the MFMA B layout: slot (nh*4 + tn)*2 + h, lane (j, q) holds
+    // k = 32 g + 8 q + 4 h .. +3 of tile column 64 nh + 16 tn + j.
+    f32x4 b[16][64];
+};
+
+__global__ __launch_bounds__(256) void q4_gemm_wide_kernel(const float* x, const uint32_t* wq, const float* ws,
+                                                          float* __restrict__ out, int M, int N, int K,
+                                                          int tiles_m, int tiles_n, int groups_per_split,
+                                                          const float* __restrict__ tmat,
+                                                          const float* __restrict__ lb, int R, float lscale) {
+    constexpr int WM = 4, WN = 4;
+    __shared__ WideLdsStage stage[2];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wid & 1;
+    const int wn = wid >> 1;
+    const int j = lane & 15;
+    const int q = lane >> 4;
+    const int G = K >> 5;
+
+    int tile_m, tile_n;
+    xcd_tile(tiles_m, tiles_n, tile_m, tile_n);
+    const int mt0 = tile_m * 128, nt0 = tile_n * 128;
+    const int m0 = mt0 + wm * 64;
+    const int n0 = nt0 + wn * 64;
+    const int g_begin = blockIdx.y * groups_per_split;
+    const int g_end = min(G, g_begin + groups_per_split);
+
+    // A copies of this wavefront: instructions 4 wid .. 4 wid + 3, each 8 full rows.
+    const float* asrc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int ins = 4 * wid + i;                  // rows 8 ins .. 8 ins + 7
+        const int pair = 4 * ins + (lane >> 4);       // row pair of this lane's 16 bytes
+        const int row_t = 2 * pair + ((lane >> 3) & 1);
+        const int c = (lane & 7) ^ (pair & 7);
+        asrc[i] = x + static_cast<size_t>(min(mt0 + row_t, M - 1)) * K + 4 * c;
+    }
+    // B: thread -> tile column bc, packed words 2 bp and 2 bp + 1 of its group bytes.
+    const int bc = tid >> 1, bp = tid & 1;
+    const uint2* bsrc = reinterpret_cast<const uint2*>(wq + static_cast<size_t>(min(nt0 + bc, N - 1)) * (K >> 3)) + bp;
+    const int bslot = ((bc >> 6) * 4 + ((bc >> 4) & 3)) * 2;
+    const int blane0 = (bc & 15) + 32 * bp;  // word 2 bp + w goes to lane (bc & 15) + 16 (2 bp + w)
+    // Scales of the lane's four MFMA columns, for the fold.
+    const float* scol[WN];
+#pragma unroll
+    for (int tn = 0; tn < WN; ++tn) scol[tn] = ws + static_cast<size_t>(min(n0 + 16 * tn + j, N - 1)) * G;
+
+    double acc[WM][WN][4];
+#pragma unroll
+    for (int tm = 0; tm < WM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < WN; ++tn)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[tm][tn][i] = 0.0;
+
+    auto issue_a = [&](int g, int st) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_global_load_lds(asrc[i] + g * 32, &stage[st].a[4 * wid + i][0], 16, 0, 0);  // 1 KiB = 8 rows
+    };
+    auto write_b = [&](uint2 pk, int st) {
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            float f[8];
+            nibbles_signed_16th(w ? pk.y : pk.x, f);
+            stage[st].b[bslot][blane0 + 16 * w] = f32x4{f[0], f[1], f[2], f[3]};
+            stage[st].b[bslot + 1][blane0 + 16 * w] = f32x4{f[4], f[5], f[6], f[7]};
+        }
+    };
+
+    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    // Two MFMA accumulator sets: group g's MFMAs go into one while the other set (group g-1)
+    // is folded into acc, so no MFMA of group g waits for the fold of group g-1.
+    auto fold = [&](const f32x4 (&P)[WM][WN], const float (&bsv)[WN]) {
+#pragma unroll
+        for (int tn = 0; tn < WN; ++tn) {
+            const double sc = static_cast<double>(bsv[tn]) * kSixteenthsUnit;
+#pragma unroll
+            for (int tm = 0; tm < WM; ++tm)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[tm][tn][i] = fma(sc, static_cast<double>(P[tm][tn][i]), acc[tm][tn][i]);
+        }
+    };
+    auto mfma_group = [&](f32x4 (&P)[WM][WN], int st) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            f32x4 av[WM], bv[WN];
+#pragma unroll
+            for (int tm = 0; tm < WM; ++tm) {
+                const int row_t = wm * 64 + 16 * tm + j;
+                const int p = row_t >> 1;
+                const f32x4* abase = &stage[st].a[0][0];
+                av[tm] = abase[p * 16 + 8 * (row_t & 1) + ((2 * q + h) ^ (p & 7))];
+            }
+#pragma unroll
+            for (int tn = 0; tn < WN; ++tn) bv[tn] = stage[st].b[(wn * 4 + tn) * 2 + h][lane];
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int tm = 0; tm < WM; ++tm)
+#pragma unroll
+                    for (int tn = 0; tn < WN; ++tn)
+                        P[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[tm][t], bv[tn][t],
+                                                                         (h == 0 && t == 0) ? zero : P[tm][tn], 0, 0, 0);
+        }
+    };
+    if (g_begin < g_end) {
+        float bs_cur[WN], bs_prev[WN];
+        f32x4 PA[WM][WN], PB[WM][WN];
+        issue_a(g_begin, 0);
+        {
+            const uint2 pk = bsrc[2 * g_begin];
+#pragma unroll
+            for (int tn = 0; tn < WN; ++tn) bs_cur[tn] = scol[tn][g_begin];
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            write_b(pk, 0);
+        }
+        __syncthreads();
+        // One step: stage group g+1, MFMAs of group g into Pc, fold of group g-1 from Pp.
+        auto step = [&](int g, f32x4 (&Pc)[WM][WN], f32x4 (&Pp)[WM][WN], bool fold_prev) {
+            const int st = (g - g_begin) & 1;
+            // The last group stages its own group again (in bounds, never read): no branch.
+            const int gn = min(g + 1, g_end - 1);
+            issue_a(gn, st ^ 1);
+            const uint2 pkn = bsrc[2 * gn];
+            float bsn[WN];
+#pragma unroll
+            for (int tn = 0; tn < WN; ++tn) bsn[tn] = scol[tn][gn];
+            mfma_group(Pc, st);
+            if (fold_prev) fold(Pp, bs_prev);
+#pragma unroll
+            for (int tn = 0; tn < WN; ++tn) bs_prev[tn] = bs_cur[tn];
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            write_b(pkn, st ^ 1);
+#pragma unroll
+            for (int tn = 0; tn < WN; ++tn) bs_cur[tn] = bsn[tn];
+            __syncthreads();
+        };
+        int g = g_begin;
+        step(g, PA, PB, false);
+        ++g;
+        for (; g + 1 < g_end; g += 2) {
+            step(g, PB, PA, true);
+            step(g + 1, PA, PB, true);
+        }
+        if (g < g_end) {
+            step(g, PB, PA, true);
+            fold(PB, bs_prev);
+        } else {
+            fold(PA, bs_prev);
+        }
+    }
+
+    if (lb != nullptr && blockIdx.y == 0) {
 #pragma unroll
         for (int tm = 0; tm < WM; ++tm) {
             const int row = min(m0 + 16 * tm + j, M - 1);
@@ -568,8 +712,9 @@ hipError_t launch_mfma(const float* x, const uint8_t* w_packed, const float* w_s
 // issue cycles whether interleaved or not).
 using SkinnyShape = TileShape<1, 4, 1, 4>;
 constexpr int kSkinnyPD = 2;
-using WideShape = TileShape<4, 4, 2, 2>;
-constexpr int kWidePD = 1;
+// Wide tile of q4_gemm_wide_kernel: 128 x 128 outputs, 4 wavefronts.
+constexpr int kWideTile = 128;
+constexpr int kWideWaves = 4;
 
 size_t align_up(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
@@ -600,9 +745,9 @@ Q4Plan plan_q4gemm(const DeviceInfo& dev, uint32_t m, uint32_t n, uint32_t k, ui
         waves_per_tile = SkinnyShape::kWaves;
     } else {
         plan.kind = Q4Plan::kWide;
-        bm = WideShape::kBM;
-        bn = WideShape::kBN;
-        waves_per_tile = WideShape::kWaves;
+        bm = kWideTile;
+        bn = kWideTile;
+        waves_per_tile = kWideWaves;
     }
     const size_t tiles = static_cast<size_t>((m + bm - 1) / bm) * ((n + bn - 1) / bn);
     const size_t waves = tiles * waves_per_tile;
@@ -673,8 +818,15 @@ hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float*
         e = launch_mfma<1, 4, 1, 4, kSkinnyPD>(x, w_packed, w_scales, out, m, n, k, plan.splits, tmat, lbp, rank,
                                                lora_scale, stream);
     } else {
-        e = launch_mfma<4, 4, 2, 2, kWidePD>(x, w_packed, w_scales, out, m, n, k, plan.splits, tmat, lbp, rank,
-                                             lora_scale, stream);
+        const int tiles_m = static_cast<int>((m + kWideTile - 1) / kWideTile);
+        const int tiles_n = static_cast<int>((n + kWideTile - 1) / kWideTile);
+        const int G = static_cast<int>(k / kGroup);
+        const int gps = (G + plan.splits - 1) / plan.splits;
+        hipLaunchKernelGGL(q4_gemm_wide_kernel, dim3(tiles_m * tiles_n, plan.splits), dim3(64 * kWideWaves), 0,
+                           stream, x, reinterpret_cast<const uint32_t*>(w_packed), w_scales, out, static_cast<int>(m),
+                           static_cast<int>(n), static_cast<int>(k), tiles_m, tiles_n, gps, tmat, lbp,
+                           static_cast<int>(rank), lora_scale);
+        e = hipGetLastError();
     }
     if (e != hipSuccess || plan.splits == 1) return e;
     const size_t count = static_cast<size_t>(m) * n;
