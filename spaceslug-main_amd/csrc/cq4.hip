@@ -67,6 +67,62 @@ __global__ __launch_bounds__(128) void cq4_transform_hadamard_kernel(Cq4View w, 
     }
 }
 
+// Hadamard basis for group sizes 64, 128 and 256 (E = gs / 64 elements per lane):
+// one wavefront per (row, group), the group held in registers. Lane l holds
+// elements l + 64 i, i < E; butterflies of stride 1..32 pair lanes l and l ^ h
+// (__shfl_xor), strides 64 and 128 pair a lane's own elements, so no LDS and no
+// barrier is involved. The right sign and permutation gather element src from
+// lane src % 64. Same arithmetic, in the same order per element, as the LDS form
+// above. Four wavefronts per workgroup cover four consecutive (row, group) pairs.
+template <int E>
+__global__ __launch_bounds__(256) void cq4_transform_hadamard_wave_kernel(Cq4View w, const uint16_t* __restrict__ a,
+                                                                          float* __restrict__ out, uint32_t pairs) {
+    constexpr uint32_t gs = 64 * E;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t pair = blockIdx.x * 4 + (threadIdx.x >> 6);  // row * num_groups + group
+    if (pair >= pairs) return;  // whole wavefronts only: no cross-lane exchange is cut short
+    const uint32_t g = pair % w.num_groups;
+    const size_t base = static_cast<size_t>(pair / w.num_groups) * w.K + static_cast<size_t>(g) * gs;
+    float v[E];
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+        const uint32_t k = lane + 64 * i;
+        const float sign = w.left_signs ? static_cast<float>(w.left_signs[k]) : 1.0f;
+        v[i] = half_bits_to_float(a[base + k]) * input_recip(w, g * gs + k) * sign;
+    }
+    for (uint32_t h = 1; h < 64; h <<= 1) {  // strides 1 .. 32 across lanes
+        const bool upper = (lane & h) != 0;
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+            const float o = __shfl_xor(v[i], static_cast<int>(h));
+            v[i] = upper ? o - v[i] : v[i] + o;
+        }
+    }
+#pragma unroll
+    for (int h = 1; h < E; h <<= 1)  // strides 64, 128 within the lane
+#pragma unroll
+        for (int i = 0; i < E; ++i)
+            if ((i & h) == 0) {
+                const float x = v[i], y = v[i + h];
+                v[i] = x + y;
+                v[i + h] = x - y;
+            }
+    const float inv = 1.0f / sqrtf(static_cast<float>(gs));
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+        const uint32_t j = lane + 64 * i;
+        const uint32_t src = w.permutation ? (w.permutation[j] & (gs - 1)) : j;
+        float x = 0.0f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const float t = __shfl(v[e], static_cast<int>(src & 63));
+            x = (src >> 6) == static_cast<uint32_t>(e) ? t : x;
+        }
+        const float sign = w.right_signs ? static_cast<float>(w.right_signs[src]) : 1.0f;
+        out[base + j] = x * inv * sign;
+    }
+}
+
 // Orthogonal basis: A_rot[m][i] = sum_k A[m][k] recip[k] R[k][i]; grid (ceil(K/256), M).
 __global__ __launch_bounds__(256) void cq4_transform_orthogonal_kernel(Cq4View w, const uint16_t* __restrict__ a,
                                                                        float* __restrict__ out) {
@@ -89,8 +145,9 @@ __device__ __forceinline__ uint32_t index_lsb(const uint8_t* p, uint32_t k, uint
 }
 
 // One thread per (column n, ROWS rows). Per group: 8 indices per 32-bit word of
-// the row's packed group, codebook values from LDS, fp32 sums per row, then
-// acc += norm(n, g) * sum.
+// the row's packed group, codebook values from LDS, fp32 sums per row over at
+// most 32 values, each folded as acc += norm(n, g) * sum in float64 (the error
+// bound of the MFMA form above).
 // LAYOUT 0: 4-bit LSB-first (nibble j of word c is k = 8c + j);
 // LAYOUT 1: 4-bit interleaved panels (row r's word c is bytes 16c + 4r .. +3:
 //           low nibble of byte b is k = 8c + b, high nibble k = 8c + 4 + b);
@@ -109,15 +166,22 @@ __global__ __launch_bounds__(256) void cq4_gemm_kernel(Cq4View w, const float* _
     const float* arow[ROWS];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) arow[r] = ap + static_cast<size_t>(min(m0 + r, M - 1)) * w.K;
-    float acc[ROWS];
+    double acc[ROWS];
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) acc[r] = 0.0f;
+    for (int r = 0; r < ROWS; ++r) acc[r] = 0.0;
     for (uint32_t g = 0; g < ng; ++g) {
         const size_t ni = inter ? (static_cast<size_t>(n / 4) * ng + g) * 4 + (n & 3) : static_cast<size_t>(n) * ng + g;
-        const float norm = half_bits_to_float(w.norms[ni]);
+        const double norm = static_cast<double>(half_bits_to_float(w.norms[ni]));
         float s[ROWS];
 #pragma unroll
         for (int r = 0; r < ROWS; ++r) s[r] = 0.0f;
+        auto fold = [&]() {
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) {
+                acc[r] = fma(norm, static_cast<double>(s[r]), acc[r]);
+                s[r] = 0.0f;
+            }
+        };
         const uint32_t kg = g * gs;
         if constexpr (LAYOUT == 2) {
             const uint8_t* p = w.packed + (static_cast<size_t>(n) * ng + g) * pgb;
@@ -125,6 +189,7 @@ __global__ __launch_bounds__(256) void cq4_gemm_kernel(Cq4View w, const float* _
                 const float cv = lut[index_lsb(p, k, w.bits)];
 #pragma unroll
                 for (int r = 0; r < ROWS; ++r) s[r] = fmaf(arow[r][kg + k], cv, s[r]);
+                if ((k & 31) == 31) fold();
             }
         } else {
             const uint8_t* base = inter ? w.packed + (static_cast<size_t>(n / 4) * ng + g) * 4 * pgb + (n & 3) * 4
@@ -151,14 +216,250 @@ __global__ __launch_bounds__(256) void cq4_gemm_kernel(Cq4View w, const float* _
 #pragma unroll
                     for (int r = 0; r < ROWS; ++r) s[r] = fmaf(av[r][kk], cv, s[r]);
                 }
+                if ((c8 & 3) == 3) fold();
             }
         }
-#pragma unroll
-        for (int r = 0; r < ROWS; ++r) acc[r] = fmaf(norm, s[r], acc[r]);
+        fold();  // the group's remainder (groups whose size is not a multiple of 32)
     }
 #pragma unroll
     for (int r = 0; r < ROWS; ++r)
-        if (m0 + r < M) c[static_cast<size_t>(m0 + r) * w.N + n] = float_to_half_bits(acc[r]);
+        if (m0 + r < M) c[static_cast<size_t>(m0 + r) * w.N + n] = float_to_half_bits(static_cast<float>(acc[r]));
+}
+
+// Up to 4 rows with 4-bit indices in either layout and word-aligned groups
+// (group size a multiple of 8): one wavefront per column, lane l taking the column's
+// 32-bit index words l, l + 64, ... (8 values each, all in one group). Per word and
+// row: 8 codebook lookups in LDS, an fp32 sum of 8 products, and norm * sum
+// accumulated in float64; the 64 lane sums are reduced in float64 across the
+// wavefront and rounded to fp16 once. At M = 1, N = 512 this keeps 512 wavefronts
+// busy where one thread per column keeps 512 threads.
+template <int ROWS, bool INTER>
+__global__ __launch_bounds__(256) void cq4_gemv_kernel(Cq4View w, const float* __restrict__ ap,
+                                                      uint16_t* __restrict__ c, uint32_t M, uint32_t gs, uint32_t ng) {
+    __shared__ float lut[16];
+    if (threadIdx.x < 16) lut[threadIdx.x] = half_bits_to_float(w.codebook[threadIdx.x]);
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t n = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (n >= w.N) return;  // whole wavefronts, after the only barrier
+    const uint32_t K = w.K, words = K >> 3, wpg = gs >> 3;
+    const size_t pgb = gs >> 1;  // bytes of one row's group
+    const float* arow[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) arow[r] = ap + static_cast<size_t>(min(static_cast<uint32_t>(r), M - 1)) * K;
+    double acc[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) acc[r] = 0.0;
+    for (uint32_t wi = lane; wi < words; wi += 64) {
+        const uint32_t g = wi / wpg, cw = wi % wpg;
+        uint32_t word;
+        size_t ni;
+        if constexpr (INTER) {  // row n & 3 of panel n / 4: its word cw at byte 16 cw + 4 (n & 3)
+            const size_t panel = static_cast<size_t>(n >> 2) * ng + g;
+            word = *reinterpret_cast<const uint32_t*>(w.packed + panel * 4 * pgb + (n & 3) * 4 + 16 * cw);
+            ni = panel * 4 + (n & 3);
+        } else {
+            const size_t grp = static_cast<size_t>(n) * ng + g;
+            word = *reinterpret_cast<const uint32_t*>(w.packed + grp * pgb + 4 * cw);
+            ni = grp;
+        }
+        float cv[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) cv[t] = lut[(word >> (4 * t)) & 0xFu];
+        const double norm = static_cast<double>(half_bits_to_float(w.norms[ni]));
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) {
+            const f32x4_t lo = *reinterpret_cast<const f32x4_t*>(arow[r] + 8 * wi);
+            const f32x4_t hi = *reinterpret_cast<const f32x4_t*>(arow[r] + 8 * wi + 4);
+            const float av[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            float sum = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                // nibble t holds k = 8 cw + t (LSB) or 8 cw + (t >> 1) + 4 (t & 1) (interleaved)
+                const int kk = INTER ? (t >> 1) + 4 * (t & 1) : t;
+                sum = fmaf(av[kk], cv[t], sum);
+            }
+            acc[r] = fma(norm, static_cast<double>(sum), acc[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) acc[r] += __shfl_xor(acc[r], off);
+    if (lane == 0)
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r)
+            if (static_cast<uint32_t>(r) < M) c[static_cast<size_t>(r) * w.N + n] = float_to_half_bits(static_cast<float>(acc[r]));
+}
+
+// MFMA form for 4-bit LSB-packed indices (the packing of cactus_x86.cpp:24-43 with
+// bits = 4: column n's K/2 bytes are contiguous, index k in the low nibble of byte
+// k/2 when k is even), a group size that is a multiple of 32 and M >= 32. The
+// weight bytes then have exactly the int4 GEMM's layout, and the int4 wide
+// kernel's design carries over: v_mfma_f32_16x16x4_f32, lane (j, q) feeding K slot
+// q with k = 8q + t at step t, so its B operands are the 8 indices of word q of a
+// 32-value sub-group. A workgroup owns a 64 x 64 tile (2 x 2 wavefronts of 32 x 32;
+// 256 workgroups at M = N = 1024) and stages two sub-groups at a time (K % 64 == 0)
+// through two LDS buffers, one barrier per pair:
+// the code-basis activations (64 rows x 32 floats) copied global -> LDS by
+// global_load_lds_dwordx4 as full 128-byte rows, XOR-swizzled within 256-byte row
+// pairs so MFMA-operand reads hit 16 bank groups; the weights decoded once per
+// workgroup (each thread one 32-bit word: 8 codebook lookups in LDS) into fp32 in
+// the MFMA B layout. The MFMA sums each 32-value sub-group in fp32, and the sub-group
+// sum times its group's norm is accumulated in float64 (exact product); C is rounded
+// to fp16 once. (The reference sums a whole group in fp32 before the norm,
+// cactus_x86.cpp:214-226: over K = 1024 that leaves errors of ~1.5e-5 near zero
+// outputs, beyond the fp16 rounding this path is held to; 32-value sums folded in
+// float64 stay under 6.2e-6 in an emulation of 131,072 outputs.)
+constexpr uint32_t kCq4MfmaMinRows = 32;
+constexpr int kCq4Tile = 64;
+constexpr int kCq4SubPerStage = 2;  // 32-value sub-groups staged per barrier
+
+struct Cq4MfmaStage {
+    // per sub-group u: row r's 16-byte chunk c (k = 32 s + 4 c .. +3) at f32x4 index
+    // (r >> 1) * 16 + 8 (r & 1) + (c ^ ((r >> 1) & 7)) of a[u]
+    f32x4_t a[kCq4SubPerStage][8 * 64];
+    // per sub-group u: slot (nh * 2 + tn) * 2 + h, lane (j, q): codebook values of
+    // k = 32 s + 8 q + 4 h .. +3 of column 32 nh + 16 tn + j
+    f32x4_t b[kCq4SubPerStage][8][64];
+};
+
+__global__ __launch_bounds__(256) void cq4_gemm_mfma_kernel(Cq4View w, const float* __restrict__ ap,
+                                                           uint16_t* __restrict__ c, uint32_t M, uint32_t gs,
+                                                           uint32_t ng, uint32_t tiles_m) {
+    __shared__ Cq4MfmaStage stage[2];
+    __shared__ float lut[16];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wid & 1, wn = wid >> 1;
+    const int j = lane & 15, q = lane >> 4;
+    const int K = static_cast<int>(w.K), N = static_cast<int>(w.N), Mi = static_cast<int>(M);
+    const int T = K / (32 * kCq4SubPerStage);      // stages (K % 64 == 0)
+    const int spg = static_cast<int>(gs) >> 5;     // sub-groups per norm group
+    const int mt0 = static_cast<int>(blockIdx.x % tiles_m) * kCq4Tile;
+    const int nt0 = static_cast<int>(blockIdx.x / tiles_m) * kCq4Tile;
+    const int m0 = mt0 + 32 * wm, n0 = nt0 + 32 * wn;
+    if (tid < 16) lut[tid] = half_bits_to_float(w.codebook[tid]);
+
+    // A copies: per sub-group, instructions 2 wid and 2 wid + 1, each 8 full rows.
+    const float* asrc[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int ins = 2 * wid + i;
+        const int pair = 4 * ins + (lane >> 4);
+        const int row_t = 2 * pair + ((lane >> 3) & 1);
+        asrc[i] = ap + static_cast<size_t>(min(mt0 + row_t, Mi - 1)) * K + 4 * ((lane & 7) ^ (pair & 7));
+    }
+    // B: thread -> tile column bc, word bw of each sub-group's 16 bytes.
+    const int bc = tid >> 2, bw = tid & 3;
+    const uint32_t* bsrc =
+        reinterpret_cast<const uint32_t*>(w.packed + static_cast<size_t>(min(nt0 + bc, N - 1)) * (K >> 1)) + bw;
+    const int bslot = ((bc >> 5) * 2 + ((bc >> 4) & 1)) * 2;
+    const int blane = (bc & 15) + 16 * bw;
+    const uint16_t* nrm[2];
+#pragma unroll
+    for (int tn = 0; tn < 2; ++tn) nrm[tn] = w.norms + static_cast<size_t>(min(n0 + 16 * tn + j, N - 1)) * ng;
+
+    auto issue_a = [&](int t, int st) {
+#pragma unroll
+        for (int u = 0; u < kCq4SubPerStage; ++u)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                __builtin_amdgcn_global_load_lds(asrc[i] + (kCq4SubPerStage * t + u) * 32,
+                                                 &stage[st].a[u][(2 * wid + i) * 64], 16, 0, 0);
+    };
+    auto load_b = [&](int t, uint32_t (&wd)[kCq4SubPerStage]) {
+#pragma unroll
+        for (int u = 0; u < kCq4SubPerStage; ++u) wd[u] = bsrc[4 * (kCq4SubPerStage * t + u)];
+    };
+    auto write_b = [&](const uint32_t (&wd)[kCq4SubPerStage], int st) {
+#pragma unroll
+        for (int u = 0; u < kCq4SubPerStage; ++u) {
+            float f[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) f[t] = lut[(wd[u] >> (4 * t)) & 0xFu];
+            stage[st].b[u][bslot][blane] = f32x4_t{f[0], f[1], f[2], f[3]};
+            stage[st].b[u][bslot + 1][blane] = f32x4_t{f[4], f[5], f[6], f[7]};
+        }
+    };
+
+    const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    double acc[2][2][4];
+#pragma unroll
+    for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < 2; ++tn)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[tm][tn][i] = 0.0;
+    __syncthreads();  // the codebook is in LDS
+    {
+        issue_a(0, 0);
+        uint32_t wd[kCq4SubPerStage];
+        load_b(0, wd);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        write_b(wd, 0);
+    }
+    __syncthreads();
+    for (int t = 0; t < T; ++t) {
+        const int st = t & 1;
+        const bool more = t + 1 < T;  // uniform
+        uint32_t wdn[kCq4SubPerStage] = {};
+        if (more) {
+            issue_a(t + 1, st ^ 1);
+            load_b(t + 1, wdn);
+        }
+#pragma unroll
+        for (int u = 0; u < kCq4SubPerStage; ++u) {
+            f32x4_t P[2][2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                f32x4_t av[2], bv[2];
+#pragma unroll
+                for (int tm = 0; tm < 2; ++tm) {
+                    const int row_t = 32 * wm + 16 * tm + j;
+                    const int pr = row_t >> 1;
+                    av[tm] = stage[st].a[u][pr * 16 + 8 * (row_t & 1) + ((2 * q + h) ^ (pr & 7))];
+                }
+#pragma unroll
+                for (int tn = 0; tn < 2; ++tn) bv[tn] = stage[st].b[u][(wn * 2 + tn) * 2 + h][lane];
+#pragma unroll
+                for (int k4 = 0; k4 < 4; ++k4)
+#pragma unroll
+                    for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+                        for (int tn = 0; tn < 2; ++tn)
+                            P[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                                av[tm][k4], bv[tn][k4], (h == 0 && k4 == 0) ? zero : P[tm][tn], 0, 0, 0);
+            }
+            const int g = (kCq4SubPerStage * t + u) / spg;
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn) {
+                const double nv = static_cast<double>(half_bits_to_float(nrm[tn][g]));
+#pragma unroll
+                for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[tm][tn][i] = fma(nv, static_cast<double>(P[tm][tn][i]), acc[tm][tn][i]);
+            }
+        }
+        if (more) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            write_b(wdn, st ^ 1);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < 2; ++tn) {
+            const int col = n0 + 16 * tn + j;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = m0 + 16 * tm + 4 * q + i;
+                if (row < Mi && col < N)
+                    c[static_cast<size_t>(row) * N + col] = float_to_half_bits(static_cast<float>(acc[tm][tn][i]));
+            }
+        }
 }
 
 template <int ROWS>
@@ -184,6 +485,15 @@ hipError_t launch_cq4_matmul(const Cq4View& w, const uint16_t* a, uint32_t m, ui
     if (orth) {
         hipLaunchKernelGGL(cq4_transform_orthogonal_kernel, dim3((w.K + 255) / 256, m), dim3(256), 0, stream, w, a,
                            workspace);
+    } else if (w.group_size == 64 || w.group_size == 128 || w.group_size == 256) {
+        const uint32_t pairs = m * w.num_groups;
+        const dim3 grid((pairs + 3) / 4);
+        if (w.group_size == 64)
+            hipLaunchKernelGGL(cq4_transform_hadamard_wave_kernel<1>, grid, dim3(256), 0, stream, w, a, workspace, pairs);
+        else if (w.group_size == 128)
+            hipLaunchKernelGGL(cq4_transform_hadamard_wave_kernel<2>, grid, dim3(256), 0, stream, w, a, workspace, pairs);
+        else
+            hipLaunchKernelGGL(cq4_transform_hadamard_wave_kernel<4>, grid, dim3(256), 0, stream, w, a, workspace, pairs);
     } else {
         // group_size / 2 threads (one for a group of 1, whose transform is the identity)
         hipLaunchKernelGGL(cq4_transform_hadamard_kernel, dim3(w.num_groups, m), dim3(w.group_size > 1 ? w.group_size / 2 : 1),
@@ -191,6 +501,24 @@ hipError_t launch_cq4_matmul(const Cq4View& w, const uint16_t* a, uint32_t m, ui
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    const bool inter = (w.flags & kCq4FlagInterleaved4Row) != 0;
+    if (m >= kCq4MfmaMinRows && w.bits == 4 && !inter && gs % 32 == 0 && w.K % (32 * kCq4SubPerStage) == 0) {
+        const uint32_t tiles_m = (m + kCq4Tile - 1) / kCq4Tile, tiles_n = (w.N + kCq4Tile - 1) / kCq4Tile;
+        hipLaunchKernelGGL(cq4_gemm_mfma_kernel, dim3(tiles_m * tiles_n), dim3(256), 0, stream, w, workspace, c, m,
+                           gs, ng, tiles_m);
+        return hipGetLastError();
+    }
+    if (m <= 4 && w.bits == 4 && gs % 8 == 0) {
+        const dim3 grid((w.N + 3) / 4);
+        if (m == 1) {
+            if (inter) hipLaunchKernelGGL((cq4_gemv_kernel<1, true>), grid, dim3(256), 0, stream, w, workspace, c, m, gs, ng);
+            else hipLaunchKernelGGL((cq4_gemv_kernel<1, false>), grid, dim3(256), 0, stream, w, workspace, c, m, gs, ng);
+        } else {
+            if (inter) hipLaunchKernelGGL((cq4_gemv_kernel<4, true>), grid, dim3(256), 0, stream, w, workspace, c, m, gs, ng);
+            else hipLaunchKernelGGL((cq4_gemv_kernel<4, false>), grid, dim3(256), 0, stream, w, workspace, c, m, gs, ng);
+        }
+        return hipGetLastError();
+    }
     return m >= 4 ? launch_gemm<4>(w, workspace, c, m, gs, ng, stream) : launch_gemm<1>(w, workspace, c, m, gs, ng, stream);
 }
 

@@ -88,6 +88,29 @@ def test_random_matrices(session, gpu, case):
     check(session, W, A, m, f"random {CASES[case]}")
 
 
+# M >= 32 with 4-bit LSB-packed indices, group sizes that are multiples of 32 and K % 64 == 0 run
+# on the MFMA kernel: ragged row and column tiles, one to several groups per row, signs,
+# permutation, both input-scale forms, the orthogonal basis, and the reference benchmark's 1024^3
+# shape; K = 96 (not a multiple of 64) at M = 48 stays on the other kernel.
+MFMA_CASES = [dict(bits=4, K=512, N=200, group_size=128, m=70),
+              dict(bits=4, K=96, N=50, group_size=32, m=48),
+              dict(bits=4, K=1024, N=96, group_size=256, signs=True, perm=True, scale="scale", m=33),
+              dict(bits=4, K=128, N=72, group_size=128, orthogonal=True, m=40),
+              dict(bits=4, K=256, N=130, group_size=32, m=64),
+              dict(bits=4, K=512, N=64, group_size=64, scale="none", m=129),
+              dict(bits=4, K=1024, N=1024, group_size=128, m=1024)]
+
+
+@pytest.mark.parametrize("case", range(len(MFMA_CASES)))
+def test_random_matrices_mfma(session, gpu, case):
+    kw = dict(MFMA_CASES[case])
+    m = kw.pop("m")
+    rng = np.random.default_rng(900 + case)
+    W = cq4.random_matrix(rng, **kw)
+    A = cq4.f16(rng.uniform(-1, 1, (m, W.K)))
+    check(session, W, A, m, f"mfma {MFMA_CASES[case]} m={m}")
+
+
 def test_device_entry_equals_host_entry(session, gpu):
     import torch
 
