@@ -224,8 +224,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void q4_gemm_mfma_kernel(
 
 // Wide tile for M > 32 (prefill, LoRA projections): 128 x 128 outputs per
 // workgroup, 2 x 2 wavefronts of 64 x 64 (4 x 4 MFMA tiles each), one wavefront
-// per SIMD (444 registers). Per 32-value group the workgroup stages, in one of
-// two LDS buffers:
+// per SIMD (289 registers; the MFMA results stay in architected VGPRs, see the
+// build's MFMA VGPR-form option, so the fold reads them without accumulator-register
+// moves). Per 32-value group the workgroup stages, in one of two LDS buffers:
 //   - the A tile (128 rows x 32 floats, 16 KiB), copied global -> LDS by
 //     global_load_lds_dwordx4 (no VGPRs): 16 copies of 8 full 128-byte rows,
 //     four per wavefront. Row chunks are XOR-swizzled so that the 16 rows a
@@ -237,7 +238,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void q4_gemm_mfma_kernel(
 // Group g+1 is staged while group g computes; one barrier per group. Against
 // the same tile with operands loaded global -> VGPR by each wavefront (every A
 // row read by both N-wavefronts, each load instruction touching half of 16
-// rows' lines, every B word decoded by both M-wavefronts): 2.34 against
+// rows' lines, every B word decoded by both M-wavefronts): 2.29-2.33 against
 // 2.41 ms at M=2048, K=4096, N=14336.
 struct WideLdsStage {
     // A tile, 128 rows x 32 floats: row r's 16-byte chunk c (k = 32 g + 4 c .. +3) at
@@ -316,8 +317,6 @@ __global__ __launch_bounds__(256) void q4_gemm_wide_kernel(const float* x, const
     };
 
     const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-    // Two MFMA accumulator sets: group g's MFMAs go into one while the other set (group g-1)
-    // is folded into acc, so no MFMA of group g waits for the fold of group g-1.
     auto fold = [&](const f32x4 (&P)[WM][WN], const float (&bsv)[WN]) {
 #pragma unroll
         for (int tn = 0; tn < WN; ++tn) {
@@ -352,8 +351,8 @@ __global__ __launch_bounds__(256) void q4_gemm_wide_kernel(const float* x, const
         }
     };
     if (g_begin < g_end) {
-        float bs_cur[WN], bs_prev[WN];
-        f32x4 PA[WM][WN], PB[WM][WN];
+        float bs_cur[WN];
+        f32x4 P[WM][WN];
         issue_a(g_begin, 0);
         {
             const uint2 pk = bsrc[2 * g_begin];
@@ -363,8 +362,7 @@ __global__ __launch_bounds__(256) void q4_gemm_wide_kernel(const float* x, const
             write_b(pk, 0);
         }
         __syncthreads();
-        // One step: stage group g+1, MFMAs of group g into Pc, fold of group g-1 from Pp.
-        auto step = [&](int g, f32x4 (&Pc)[WM][WN], f32x4 (&Pp)[WM][WN], bool fold_prev) {
+        for (int g = g_begin; g < g_end; ++g) {
             const int st = (g - g_begin) & 1;
             // The last group stages its own group again (in bounds, never read): no branch.
             const int gn = min(g + 1, g_end - 1);
@@ -373,28 +371,13 @@ __global__ __launch_bounds__(256) void q4_gemm_wide_kernel(const float* x, const
             float bsn[WN];
 #pragma unroll
             for (int tn = 0; tn < WN; ++tn) bsn[tn] = scol[tn][gn];
-            mfma_group(Pc, st);
-            if (fold_prev) fold(Pp, bs_prev);
-#pragma unroll
-            for (int tn = 0; tn < WN; ++tn) bs_prev[tn] = bs_cur[tn];
+            mfma_group(P, st);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             write_b(pkn, st ^ 1);
+            __syncthreads();
+            fold(P, bs_cur);  // P is in registers: the fold needs no LDS
 #pragma unroll
             for (int tn = 0; tn < WN; ++tn) bs_cur[tn] = bsn[tn];
-            __syncthreads();
-        };
-        int g = g_begin;
-        step(g, PA, PB, false);
-        ++g;
-        for (; g + 1 < g_end; g += 2) {
-            step(g, PB, PA, true);
-            step(g + 1, PA, PB, true);
-        }
-        if (g < g_end) {
-            step(g, PB, PA, true);
-            fold(PB, bs_prev);
-        } else {
-            fold(PA, bs_prev);
         }
     }
 
