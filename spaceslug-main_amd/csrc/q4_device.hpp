@@ -57,6 +57,24 @@ __device__ __forceinline__ void nibbles_signed_16th_mfma(uint32_t w, float (&f)[
 // Scale that restores nibbles_signed_16th's values to the integers v.
 constexpr float kSixteenthsUnit = 16.0f;
 
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// The 8 nibbles of w as bf16 v / 16, packed in element order (element t in the
+// low half of word t/2 when t is even, the high half when odd). v / 16 has at
+// most three significant bits, so the high half of its fp32 form is the exact
+// bf16 value and one byte permute packs two. For values written to LDS: the
+// consumer is a later MFMA, not the next instruction, so the inline-asm decode
+// is safe here.
+__device__ __forceinline__ u32x4 nibbles_bf16_16th(uint32_t w) {
+    float f[8];
+    nibbles_signed_16th(w, f);
+    u32x4 r;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+        r[t] = __builtin_amdgcn_perm(__float_as_uint(f[2 * t + 1]), __float_as_uint(f[2 * t]), 0x07060302u);
+    return r;
+}
+
 // The four 16-lane rows of a wavefront as a 4 x 4 transpose of 32-bit values:
 // on return, register c of row q holds what register q of row c held.
 // v_permlane32_swap exchanges rows 2-3 of its first operand with rows 0-1 of

@@ -1,22 +1,24 @@
-// fp32-MFMA int4 GEMM for 5+ rows (prefill, small-batch decode, LoRA projections).
+// MFMA int4 GEMM for 5+ rows (prefill, small-batch decode, LoRA projections).
 // Three kernels: q4_gemm_wide_kernel for M > 32, q4_gemm_skinny_kernel for
 // M <= 32 with K % 128 == 0 and q4_gemm_mfma_kernel (K-split) for the other
 // M <= 32 shapes, each described at its definition.
 //
 // Replaces q4gemm.comp:61-175 (64x64 tile, LDS-staged dequantised B, 4x4 FMA
-// micro-tile per thread) with a CDNA4 design built on v_mfma_f32_16x16x4_f32.
+// micro-tile per thread) with a CDNA4 design on the matrix cores: the two
+// small-M kernels on v_mfma_f32_16x16x4_f32, the wide kernel on
+// v_mfma_f32_16x16x32_bf16 with x split exactly into three bf16 limbs.
 // Common to all three:
 //   - per 32-value scale group, lane (j = l%16, q = l/16) feeds the MFMA K slot
-//     q with k = 8q + t at step t = 0..7, so its B operands for column j are
-//     the 8 nibbles of ONE 32-bit word of the packed column (word q of the
-//     group's 16 bytes) and its A operands are 8 consecutive floats of row j.
-//     Weights are decoded to v / 16 (v_cvt_off_f32_i4, exact; the factor 16
-//     joins the scale);
-//   - the MFMA accumulates P = x * v over one group (8 steps) in fp32 from
-//     zero, and the group is folded into a float64 accumulator as
-//     acc += (double)s * P. Scale application moves out of the inner loop, and
-//     the long K sum is carried in double, which keeps the max relative error
-//     against the double-precision reference well under 1e-5 at K = 4096;
+//     q with k = 8q .. 8q + 7, so its B operands for column j are the 8 nibbles
+//     of ONE 32-bit word of the packed column (word q of the group's 16 bytes)
+//     and its A operands are 8 consecutive values of row j. Weights are decoded
+//     to v / 16 (v_cvt_off_f32_i4, exact; the factor 16 joins the scale);
+//   - every product x * v / 16 is exact in fp32; the MFMA accumulates
+//     P = sum x * v / 16 over one group in fp32 from zero, and the group is
+//     folded into a float64 accumulator as acc += (double)(16 s) * P. Scale
+//     application moves out of the inner loop, and the long K sum is carried in
+//     double, which keeps the max relative error against the double-precision
+//     reference well under 1e-5 at K = 4096;
 //   - large grids are XCD-aware: workgroup ids are remapped so each of the 8
 //     XCDs (one L2 each) walks a contiguous band of output tiles, sharing A
 //     rows and weight columns within its L2;
@@ -222,36 +224,104 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void q4_gemm_mfma_kernel(
     }
 }
 
+// Limbs per x value on the bf16 MFMA path.
+constexpr int kLimbs = 3;
+
+// x (fp32, M x K) -> x limbs (bf16, [M][KB][3][64] with KB = ceil(K / 64), rows
+// zero-padded to KB * 64 values) for q4_gemm_wide_kernel. Each value is split
+// exactly: b0 = x truncated to bf16 (the top 8 significant bits, so never
+// rounded up past the fp32 range), b1 = (x - b0) truncated the same way, and
+// b2 = x - b0 - b1, which has at most 8 significant bits and is exact in bf16;
+// both subtractions are exact in fp32. So b0 + b1 + b2 == x for every finite x,
+// and a product of a limb with a bf16 weight v/16 is exact in fp32.
+// One thread per 8 consecutive values of a row: two 16-byte loads, three
+// 16-byte stores (one per limb), coalesced along the row.
+__global__ __launch_bounds__(256) void split_x_kernel(const float* __restrict__ x, uint16_t* __restrict__ xs,
+                                                      int M, int K, int KB) {
+    const size_t idx = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+    const size_t per_row = static_cast<size_t>(KB) * 8;
+    if (idx >= static_cast<size_t>(M) * per_row) return;
+    const int row = static_cast<int>(idx / per_row);
+    const int c8 = static_cast<int>(idx % per_row);
+    const int kb = c8 >> 3, c = c8 & 7;
+    const int k0 = kb * 64 + c * 8;
+    float v[8];
+    if (k0 < K) {  // K % 32 == 0, so the 8 values are all inside the row or all past it
+        const f32x4 lo = *reinterpret_cast<const f32x4*>(x + static_cast<size_t>(row) * K + k0);
+        const f32x4 hi = *reinterpret_cast<const f32x4*>(x + static_cast<size_t>(row) * K + k0 + 4);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            v[t] = lo[t];
+            v[t + 4] = hi[t];
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) v[t] = 0.0f;
+    }
+    u32x4 limb[kLimbs];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        uint32_t bits[kLimbs][2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const float b0 = __uint_as_float(__float_as_uint(v[2 * t + e]) & 0xFFFF0000u);
+            const float r1 = v[2 * t + e] - b0;
+            const float b1 = __uint_as_float(__float_as_uint(r1) & 0xFFFF0000u);
+            const float r2 = r1 - b1;
+            bits[0][e] = __float_as_uint(b0) >> 16;
+            bits[1][e] = __float_as_uint(b1) >> 16;
+            bits[2][e] = __float_as_uint(r2) >> 16;
+        }
+#pragma unroll
+        for (int li = 0; li < kLimbs; ++li) limb[li][t] = bits[li][0] | (bits[li][1] << 16);
+    }
+    uint16_t* dst = xs + (static_cast<size_t>(row) * KB + kb) * (kLimbs * 64) + c * 8;
+#pragma unroll
+    for (int li = 0; li < kLimbs; ++li) *reinterpret_cast<u32x4*>(dst + li * 64) = limb[li];
+}
+
 // Wide tile for M > 32 (prefill, LoRA projections): 128 x 128 outputs per
 // workgroup, 2 x 2 wavefronts of 64 x 64 (4 x 4 MFMA tiles each), one wavefront
-// per SIMD (289 registers; the MFMA results stay in architected VGPRs, see the
-// build's MFMA VGPR-form option, so the fold reads them without accumulator-register
-// moves). Per 32-value group the workgroup stages, in one of two LDS buffers:
-//   - the A tile (128 rows x 32 floats, 16 KiB), copied global -> LDS by
-//     global_load_lds_dwordx4 (no VGPRs): 16 copies of 8 full 128-byte rows,
-//     four per wavefront. Row chunks are XOR-swizzled so that the 16 rows a
-//     pass of MFMA-operand reads touches fall on 16 distinct bank groups;
-//   - the dequantised B tile (128 columns x 32 values as v/16 floats, 16 KiB):
-//     each thread loads 8 packed bytes (two words of one column), decodes them
-//     once for the whole workgroup, and writes them in the MFMA B layout, so
-//     every wavefront reads its B operands as linear 1 KiB runs.
-// Group g+1 is staged while group g computes; one barrier per group. Against
-// the same tile with operands loaded global -> VGPR by each wavefront (every A
-// row read by both N-wavefronts, each load instruction touching half of 16
-// rows' lines, every B word decoded by both M-wavefronts): 2.29-2.33 against
-// 2.41 ms at M=2048, K=4096, N=14336.
+// per SIMD. The matrix instruction is v_mfma_f32_16x16x32_bf16, fed with x as
+// three exact bf16 limbs (split_x_kernel) and the weights as bf16 v/16 (exact):
+// every product is exact in fp32, each 32-value group's sum P = sum x * v/16 is
+// accumulated in fp32 by three chained MFMAs (smallest limb first), and the
+// group is folded into a float64 accumulator as acc += (double)(16 s) * P, as on
+// the other GEMM paths. One such MFMA (16 x 16 x 32) does the work of eight
+// fp32 16x16x4 MFMAs at a sixteenth of their matrix-core cycles each, so three
+// of them cost under a fifth of the fp32 form.
+// Lane (j = l%16, q = l/16) of a 16x16x32 MFMA holds A[row j][k = 8q .. 8q+7] and
+// B[k = 8q .. 8q+7][column j] (8 bf16 each), and result rows 4q .. 4q+3 of column
+// j. Per stage of two groups (64 values of K) the workgroup fills one of two LDS
+// buffers (64 KiB each):
+//   - the x-limb tile (3 limbs x 128 rows x 64 values, 48 KiB), copied global ->
+//     LDS by global_load_lds_dwordx4 (no VGPRs): per limb 16 copies of 8 full
+//     128-byte rows, four rows' blocks per wavefront with the three limbs at
+//     fixed offsets. Row chunks are XOR-swizzled so that the 16 rows a pass of
+//     MFMA-operand reads touches fall on 16 distinct bank groups;
+//   - the dequantised B tile (2 groups x 128 columns x 32 values as bf16 v/16,
+//     16 KiB): each thread loads one group's 16 packed bytes of one column,
+//     decodes them once for the whole workgroup and writes them in the MFMA B
+//     layout, so every wavefront reads its B operands as linear 1 KiB runs.
+// Stage s+1 is copied while stage s computes; one barrier per stage. An odd
+// number of groups leaves the last stage's second group empty: its x limbs are
+// zero padding, its weight loads are clamped into the column, and its MFMAs and
+// fold are skipped (a wavefront-uniform branch). Against the same tile on
+// v_mfma_f32_16x16x4_f32 with x staged as fp32 (the previous product kernel):
+// 1.34 against 2.28-2.32 ms at M=2048, K=4096, N=14336 and 111 against 179 us at
+// M=512, K=N=4096, same box.
 struct WideLdsStage {
-    // A tile, 128 rows x 32 floats: row r's 16-byte chunk c (k = 32 g + 4 c .. +3) at
-    // f32x4 index (r >> 1) * 16 + 8 * (r & 1) + (c ^ ((r >> 1) & 7)).
-    f32x4 a[16][64];
-    // B tile, v/16 floats in the MFMA B layout: slot (nh*4 + tn)*2 + h, lane (j, q) holds
-    // k = 32 g + 8 q + 4 h .. +3 of tile column 64 nh + 16 tn + j.
-    f32x4 b[16][64];
+    // Limb li, 8-row copy block, lane slot: row r's 16-byte chunk c (k = 64 kb + 8 c .. +7)
+    // at u32x4 index (r >> 1) * 16 + 8 * (r & 1) + (c ^ ((r >> 1) & 7)) of a[li].
+    u32x4 a[kLimbs][16][64];
+    // Group h of the stage, 16-column tile, lane (j, q): bf16 v/16 of k = 32 (2 kb + h) + 8 q .. +7
+    // of tile column 16 * tile + j.
+    u32x4 b[2][8][64];
 };
 
-__global__ __launch_bounds__(256) void q4_gemm_wide_kernel(const float* x, const uint32_t* wq, const float* ws,
+__global__ __launch_bounds__(256) void q4_gemm_wide_kernel(const uint16_t* xs, const uint32_t* wq, const float* ws,
                                                           float* __restrict__ out, int M, int N, int K,
-                                                          int tiles_m, int tiles_n, int groups_per_split,
+                                                          int tiles_m, int tiles_n, int stages_per_split,
                                                           const float* __restrict__ tmat,
                                                           const float* __restrict__ lb, int R, float lscale) {
     constexpr int WM = 4, WN = 4;
@@ -264,30 +334,29 @@ __global__ __launch_bounds__(256) void q4_gemm_wide_kernel(const float* x, const
     const int j = lane & 15;
     const int q = lane >> 4;
     const int G = K >> 5;
+    const int KB = (G + 1) >> 1;
 
     int tile_m, tile_n;
     xcd_tile(tiles_m, tiles_n, tile_m, tile_n);
     const int mt0 = tile_m * 128, nt0 = tile_n * 128;
     const int m0 = mt0 + wm * 64;
     const int n0 = nt0 + wn * 64;
-    const int g_begin = blockIdx.y * groups_per_split;
-    const int g_end = min(G, g_begin + groups_per_split);
+    const int kb_begin = blockIdx.y * stages_per_split;
+    const int kb_end = min(KB, kb_begin + stages_per_split);
 
-    // A copies of this wavefront: instructions 4 wid .. 4 wid + 3, each 8 full rows.
-    const float* asrc[4];
+    // x-limb copies of this wavefront: 8-row blocks 4 wid .. 4 wid + 3, three limbs each.
+    const uint16_t* asrc[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int ins = 4 * wid + i;                  // rows 8 ins .. 8 ins + 7
-        const int pair = 4 * ins + (lane >> 4);       // row pair of this lane's 16 bytes
+        const int blk = 4 * wid + i;
+        const int pair = 4 * blk + (lane >> 4);  // row pair of this lane's 16 bytes
         const int row_t = 2 * pair + ((lane >> 3) & 1);
         const int c = (lane & 7) ^ (pair & 7);
-        asrc[i] = x + static_cast<size_t>(min(mt0 + row_t, M - 1)) * K + 4 * c;
+        asrc[i] = xs + static_cast<size_t>(min(mt0 + row_t, M - 1)) * KB * (kLimbs * 64) + 8 * c;
     }
-    // B: thread -> tile column bc, packed words 2 bp and 2 bp + 1 of its group bytes.
-    const int bc = tid >> 1, bp = tid & 1;
-    const uint2* bsrc = reinterpret_cast<const uint2*>(wq + static_cast<size_t>(min(nt0 + bc, N - 1)) * (K >> 3)) + bp;
-    const int bslot = ((bc >> 6) * 4 + ((bc >> 4) & 3)) * 2;
-    const int blane0 = (bc & 15) + 32 * bp;  // word 2 bp + w goes to lane (bc & 15) + 16 (2 bp + w)
+    // B: thread -> tile column bc, group bh of the stage (16 bytes = 4 packed words).
+    const int bc = tid & 127, bh = tid >> 7;
+    const u32x4* bsrc = reinterpret_cast<const u32x4*>(wq + static_cast<size_t>(min(nt0 + bc, N - 1)) * (K >> 3));
     // Scales of the lane's four MFMA columns, for the fold.
     const float* scol[WN];
 #pragma unroll
@@ -301,18 +370,24 @@ __global__ __launch_bounds__(256) void q4_gemm_wide_kernel(const float* x, const
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[tm][tn][i] = 0.0;
 
-    auto issue_a = [&](int g, int st) {
+    auto issue_a = [&](int kb, int st) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            __builtin_amdgcn_global_load_lds(asrc[i] + g * 32, &stage[st].a[4 * wid + i][0], 16, 0, 0);  // 1 KiB = 8 rows
-    };
-    auto write_b = [&](uint2 pk, int st) {
 #pragma unroll
-        for (int w = 0; w < 2; ++w) {
-            float f[8];
-            nibbles_signed_16th(w ? pk.y : pk.x, f);
-            stage[st].b[bslot][blane0 + 16 * w] = f32x4{f[0], f[1], f[2], f[3]};
-            stage[st].b[bslot + 1][blane0 + 16 * w] = f32x4{f[4], f[5], f[6], f[7]};
+            for (int li = 0; li < kLimbs; ++li)  // 1 KiB = 8 rows of one limb
+                __builtin_amdgcn_global_load_lds(asrc[i] + static_cast<size_t>(kb) * (kLimbs * 64) + li * 64,
+                                                 &stage[st].a[li][4 * wid + i][0], 16, 0, 0);
+    };
+    auto load_b = [&](int kb) { return bsrc[min(2 * kb + bh, G - 1)]; };
+    auto write_b = [&](u32x4 pk, int st) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) stage[st].b[bh][bc >> 4][(bc & 15) + 16 * w] = nibbles_bf16_16th(pk[w]);
+    };
+    auto load_s = [&](int kb, float (&s)[2][WN]) {
+#pragma unroll
+        for (int tn = 0; tn < WN; ++tn) {
+            s[0][tn] = scol[tn][2 * kb];
+            s[1][tn] = scol[tn][min(2 * kb + 1, G - 1)];
         }
     };
 
@@ -327,57 +402,57 @@ __global__ __launch_bounds__(256) void q4_gemm_wide_kernel(const float* x, const
                 for (int i = 0; i < 4; ++i) acc[tm][tn][i] = fma(sc, static_cast<double>(P[tm][tn][i]), acc[tm][tn][i]);
         }
     };
-    auto mfma_group = [&](f32x4 (&P)[WM][WN], int st) {
+    auto mfma_group = [&](f32x4 (&P)[WM][WN], int st, int h) {
+        bf16x8 bv[WN];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            f32x4 av[WM], bv[WN];
+        for (int tn = 0; tn < WN; ++tn) bv[tn] = __builtin_bit_cast(bf16x8, stage[st].b[h][wn * 4 + tn][lane]);
 #pragma unroll
-            for (int tm = 0; tm < WM; ++tm) {
-                const int row_t = wm * 64 + 16 * tm + j;
-                const int p = row_t >> 1;
-                const f32x4* abase = &stage[st].a[0][0];
-                av[tm] = abase[p * 16 + 8 * (row_t & 1) + ((2 * q + h) ^ (p & 7))];
+        for (int tm = 0; tm < WM; ++tm) {
+            const int row_t = wm * 64 + 16 * tm + j;
+            const int p = row_t >> 1;
+            const int idx = p * 16 + 8 * (row_t & 1) + ((4 * h + q) ^ (p & 7));
+            bf16x8 av[kLimbs];
+#pragma unroll
+            for (int li = 0; li < kLimbs; ++li) av[li] = __builtin_bit_cast(bf16x8, (&stage[st].a[li][0][0])[idx]);
+#pragma unroll
+            for (int tn = 0; tn < WN; ++tn) {
+                f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[2], bv[tn], zero, 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[1], bv[tn], t, 0, 0, 0);
+                P[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[0], bv[tn], t, 0, 0, 0);
             }
-#pragma unroll
-            for (int tn = 0; tn < WN; ++tn) bv[tn] = stage[st].b[(wn * 4 + tn) * 2 + h][lane];
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-#pragma unroll
-                for (int tm = 0; tm < WM; ++tm)
-#pragma unroll
-                    for (int tn = 0; tn < WN; ++tn)
-                        P[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[tm][t], bv[tn][t],
-                                                                         (h == 0 && t == 0) ? zero : P[tm][tn], 0, 0, 0);
         }
     };
-    if (g_begin < g_end) {
-        float bs_cur[WN];
+    if (kb_begin < kb_end) {
+        float bs_cur[2][WN];
         f32x4 P[WM][WN];
-        issue_a(g_begin, 0);
+        issue_a(kb_begin, 0);
         {
-            const uint2 pk = bsrc[2 * g_begin];
-#pragma unroll
-            for (int tn = 0; tn < WN; ++tn) bs_cur[tn] = scol[tn][g_begin];
+            const u32x4 pk = load_b(kb_begin);
+            load_s(kb_begin, bs_cur);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             write_b(pk, 0);
         }
         __syncthreads();
-        for (int g = g_begin; g < g_end; ++g) {
-            const int st = (g - g_begin) & 1;
-            // The last group stages its own group again (in bounds, never read): no branch.
-            const int gn = min(g + 1, g_end - 1);
-            issue_a(gn, st ^ 1);
-            const uint2 pkn = bsrc[2 * gn];
-            float bsn[WN];
-#pragma unroll
-            for (int tn = 0; tn < WN; ++tn) bsn[tn] = scol[tn][gn];
-            mfma_group(P, st);
+        for (int kb = kb_begin; kb < kb_end; ++kb) {
+            const int st = (kb - kb_begin) & 1;
+            // The last stage copies its own stage again (in bounds, never read): no branch.
+            const int kbn = min(kb + 1, kb_end - 1);
+            issue_a(kbn, st ^ 1);
+            const u32x4 pkn = load_b(kbn);
+            float bsn[2][WN];
+            load_s(kbn, bsn);
+            const bool second = 2 * kb + 1 < G;
+            mfma_group(P, st, 0);
+            fold(P, bs_cur[0]);
+            if (second) mfma_group(P, st, 1);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             write_b(pkn, st ^ 1);
             __syncthreads();
-            fold(P, bs_cur);  // P is in registers: the fold needs no LDS
+            if (second) fold(P, bs_cur[1]);  // P is in registers: the fold needs no LDS
 #pragma unroll
-            for (int tn = 0; tn < WN; ++tn) bs_cur[tn] = bsn[tn];
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int tn = 0; tn < WN; ++tn) bs_cur[h][tn] = bsn[h][tn];
         }
     }
 
@@ -685,14 +760,9 @@ hipError_t launch_mfma(const float* x, const uint8_t* w_packed, const float* w_s
     return hipGetLastError();
 }
 
-// Tile shapes of q4_gemm_mfma_kernel: skinny split-K (M <= 32 with K not a
-// multiple of 128) = one 16-row MFMA tile x 256 columns per workgroup (4 waves
-// of 16 x 64), 2 groups in flight; wide = 128 x 128 per workgroup (2 x 2 waves of
-// 64 x 64), 1 group in flight (register bound: 64 double accumulators + 64
-// MFMA accumulators per lane). Measured slower at M=2048: 64 x 32 wave tiles
-// at two waves per SIMD, a second MFMA accumulator set, and the flush split
-// in halves interleaved with the MFMAs (VALU instructions cost matrix-core
-// issue cycles whether interleaved or not).
+// Tile shape of q4_gemm_mfma_kernel (M <= 32 with K not a multiple of 128): one
+// 16-row MFMA tile x 256 columns per workgroup (4 waves of 16 x 64), 2 groups in
+// flight.
 using SkinnyShape = TileShape<1, 4, 1, 4>;
 constexpr int kSkinnyPD = 2;
 // Wide tile of q4_gemm_wide_kernel: 128 x 128 outputs, 4 wavefronts.
@@ -700,6 +770,11 @@ constexpr int kWideTile = 128;
 constexpr int kWideWaves = 4;
 
 size_t align_up(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+// Bytes of the wide kernel's x limbs: M rows x ceil(K / 64) stages x 3 limbs x 64 bf16.
+size_t wide_limb_bytes(uint32_t m, uint32_t k) {
+    return static_cast<size_t>(m) * ((k / kGroup + 1) / 2) * kLimbs * 64 * sizeof(uint16_t);
+}
 
 }  // namespace
 
@@ -740,11 +815,13 @@ Q4Plan plan_q4gemm(const DeviceInfo& dev, uint32_t m, uint32_t n, uint32_t k, ui
     const int min_groups = plan.kind == Q4Plan::kSkinnySplitK ? 8 : 4;
     int splits = 1;
     while (waves * splits * 2 <= target && groups / (splits * 2) >= min_groups) splits *= 2;
-    // Re-derive so that no split is empty.
-    const int gps = (groups + splits - 1) / splits;
-    splits = (groups + gps - 1) / gps;
+    // Re-derive so that no split is empty. The wide kernel splits whole stages of two groups.
+    const int units = plan.kind == Q4Plan::kWide ? (groups + 1) / 2 : groups;
+    const int per_split = (units + splits - 1) / splits;
+    splits = (units + per_split - 1) / per_split;
     plan.splits = splits;
     size_t bytes = lora_bytes;
+    if (plan.kind == Q4Plan::kWide) bytes += align_up(wide_limb_bytes(m, k));  // x limbs
     if (splits > 1) bytes += align_up(static_cast<size_t>(splits) * m * n * sizeof(float));
     plan.workspace_bytes = bytes;
     return plan;
@@ -767,6 +844,7 @@ hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float*
         float* tpart = reinterpret_cast<float*>(wsp);
         wsp += align_up(static_cast<size_t>(plan.t_splits) * m * rank * sizeof(float));
         tmat = reinterpret_cast<float*>(wsp);
+        wsp += align_up(static_cast<size_t>(m) * rank * sizeof(float));
         hipLaunchKernelGGL(lora_t_kernel, dim3((m + 15) / 16, (rank + 15) / 16, plan.t_splits), dim3(64), 0, stream,
                            x, la, tpart, static_cast<int>(m), static_cast<int>(k), static_cast<int>(rank));
         hipError_t e = hipGetLastError();
@@ -803,11 +881,17 @@ hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float*
     } else {
         const int tiles_m = static_cast<int>((m + kWideTile - 1) / kWideTile);
         const int tiles_n = static_cast<int>((n + kWideTile - 1) / kWideTile);
-        const int G = static_cast<int>(k / kGroup);
-        const int gps = (G + plan.splits - 1) / plan.splits;
+        const int KB = static_cast<int>((k / kGroup + 1) / 2);
+        const int stages_per_split = (KB + plan.splits - 1) / plan.splits;
+        uint16_t* xs = reinterpret_cast<uint16_t*>(wsp);
+        const size_t chunks = static_cast<size_t>(m) * KB * 8;
+        hipLaunchKernelGGL(split_x_kernel, dim3(static_cast<unsigned>((chunks + 255) / 256)), dim3(256), 0, stream, x,
+                           xs, static_cast<int>(m), static_cast<int>(k), KB);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
         hipLaunchKernelGGL(q4_gemm_wide_kernel, dim3(tiles_m * tiles_n, plan.splits), dim3(64 * kWideWaves), 0,
-                           stream, x, reinterpret_cast<const uint32_t*>(w_packed), w_scales, out, static_cast<int>(m),
-                           static_cast<int>(n), static_cast<int>(k), tiles_m, tiles_n, gps, tmat, lbp,
+                           stream, xs, reinterpret_cast<const uint32_t*>(w_packed), w_scales, out, static_cast<int>(m),
+                           static_cast<int>(n), static_cast<int>(k), tiles_m, tiles_n, stages_per_split, tmat, lbp,
                            static_cast<int>(rank), lora_scale);
         e = hipGetLastError();
     }

@@ -22,7 +22,7 @@ struct Q4Plan {
     // inside the workgroup; kSkinnySplitK: other m <= 32; kWide: m > 32.
     enum Kind { kGemv, kSkinny, kSkinnySplitK, kWide } kind;
     int splits;              // K-splits of the MFMA kernel (1 = write y directly)
-    size_t workspace_bytes;  // device scratch the call needs (split partials, LoRA T partials and T)
+    size_t workspace_bytes;  // device scratch the call needs (split partials, LoRA T partials and T, x limbs)
     int t_splits;            // K-splits of the LoRA pre-pass T = x * lora_a (0 without LoRA)
 };
 
