@@ -93,9 +93,10 @@ int spaceslug_q4gemm_lora(const float* x, const uint8_t* w_packed, const float* 
  * counterpart: the reference never passes device memory across its ABI).
  * d_x, d_w_packed must be 16-byte aligned; d_w_scales, d_y 4-byte aligned.
  * Enqueues only. The m <= 4 decode path uses no device memory beyond its
- * arguments; the MFMA path, when it splits K across workgroups, keeps its
- * partial sums in a library-owned device workspace that is allocated on first
- * use and grown on demand (growth synchronises the device, steady state does
+ * arguments; the MFMA path keeps K-split partial sums, and for m > 32 the
+ * three bf16 limbs of x (6 * m * k bytes, k rounded up to a multiple of 64), in
+ * a library-owned device workspace that is allocated on first use and grown on
+ * demand (growth synchronises the device, steady state does
  * not allocate). Calls that share a device share that workspace; the library
  * orders them: a call on a stream other than the previous user's makes its
  * stream wait (on the GPU, hipStreamWaitEvent) for that user's kernels, and
