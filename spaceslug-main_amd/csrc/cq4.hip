@@ -6,7 +6,8 @@
 //   1. the activation transform writes the code-basis activations A' in fp32
 //      (one workgroup per (row, group) for the Hadamard basis: scale and left
 //      sign, an in-LDS normalized Walsh-Hadamard transform, right sign and
-//      permutation; a direct product with the rotation for the orthogonal mode);
+//      permutation; a direct product with the rotation for the orthogonal mode),
+//      or, for the MFMA GEMM, each value as three exact bf16 limbs;
 //   2. one GEMM kernel decodes the packed indices in registers (LSB-first bit
 //      packing or 4-row interleaved panels), looks codebook values up in LDS and
 //      accumulates in fp32 per group, scaling each group sum by its norm; the
@@ -17,6 +18,7 @@
 #include <cstdint>
 
 #include "cq4_kernels.hpp"
+#include "q4_device.hpp"
 
 namespace spaceslug {
 namespace {
@@ -34,10 +36,26 @@ __device__ __forceinline__ float input_recip(const Cq4View& w, uint32_t k) {
     return 1.0f;
 }
 
+// Stores the code-basis value x of (row, k): as fp32 into out[row][k], or, when xs is set
+// (the MFMA path, K % 64 == 0), as its three exact bf16 limbs in the limb layout
+// [M][K/64][3][64] that cq4_gemm_mfma_kernel copies to LDS.
+__device__ __forceinline__ void store_code(float* out, uint16_t* xs, uint32_t K, size_t row, uint32_t k, float x) {
+    if (xs == nullptr) {
+        out[row * K + k] = x;
+        return;
+    }
+    uint32_t b[3];
+    split_bf16_limbs(x, b);
+    uint16_t* d = xs + (row * (K >> 6) + (k >> 6)) * (3 * 64) + (k & 63);
+    d[0] = static_cast<uint16_t>(b[0]);
+    d[64] = static_cast<uint16_t>(b[1]);
+    d[128] = static_cast<uint16_t>(b[2]);
+}
+
 // Hadamard basis: grid (num_groups, M), group_size / 2 threads; thread t owns
 // elements t and t + gs/2 on load and store and butterfly t at every stage.
 __global__ __launch_bounds__(128) void cq4_transform_hadamard_kernel(Cq4View w, const uint16_t* __restrict__ a,
-                                                                     float* __restrict__ out) {
+                                                                     float* __restrict__ out, uint16_t* __restrict__ xs) {
     __shared__ float v[256];
     const uint32_t gs = w.group_size, half = gs >> 1;
     const uint32_t g = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
@@ -63,7 +81,7 @@ __global__ __launch_bounds__(128) void cq4_transform_hadamard_kernel(Cq4View w, 
         // an out-of-range entry is masked into the group (the host entry point rejects it)
         const uint32_t src = w.permutation ? (w.permutation[j] & (gs - 1)) : j;
         const float sign = w.right_signs ? static_cast<float>(w.right_signs[src]) : 1.0f;
-        out[row + j] = v[src] * inv * sign;
+        store_code(out, xs, w.K, m, g * gs + j, v[src] * inv * sign);
     }
 }
 
@@ -76,7 +94,8 @@ __global__ __launch_bounds__(128) void cq4_transform_hadamard_kernel(Cq4View w, 
 // above. Four wavefronts per workgroup cover four consecutive (row, group) pairs.
 template <int E>
 __global__ __launch_bounds__(256) void cq4_transform_hadamard_wave_kernel(Cq4View w, const uint16_t* __restrict__ a,
-                                                                          float* __restrict__ out, uint32_t pairs) {
+                                                                          float* __restrict__ out, uint16_t* __restrict__ xs,
+                                                                          uint32_t pairs) {
     constexpr uint32_t gs = 64 * E;
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t pair = blockIdx.x * 4 + (threadIdx.x >> 6);  // row * num_groups + group
@@ -119,13 +138,13 @@ __global__ __launch_bounds__(256) void cq4_transform_hadamard_wave_kernel(Cq4Vie
             x = (src >> 6) == static_cast<uint32_t>(e) ? t : x;
         }
         const float sign = w.right_signs ? static_cast<float>(w.right_signs[src]) : 1.0f;
-        out[base + j] = x * inv * sign;
+        store_code(out, xs, w.K, pair / w.num_groups, g * gs + j, x * inv * sign);
     }
 }
 
 // Orthogonal basis: A_rot[m][i] = sum_k A[m][k] recip[k] R[k][i]; grid (ceil(K/256), M).
 __global__ __launch_bounds__(256) void cq4_transform_orthogonal_kernel(Cq4View w, const uint16_t* __restrict__ a,
-                                                                       float* __restrict__ out) {
+                                                                       float* __restrict__ out, uint16_t* __restrict__ xs) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x, m = blockIdx.y;
     if (i >= w.K) return;
     const uint16_t* arow = a + static_cast<size_t>(m) * w.K;
@@ -133,7 +152,7 @@ __global__ __launch_bounds__(256) void cq4_transform_orthogonal_kernel(Cq4View w
     for (uint32_t k = 0; k < w.K; ++k)
         acc = fmaf(half_bits_to_float(arow[k]) * input_recip(w, k), half_bits_to_float(w.rotation[static_cast<size_t>(k) * w.K + i]),
                    acc);
-    out[static_cast<size_t>(m) * w.K + i] = acc;
+    store_code(out, xs, w.K, m, i, acc);
 }
 
 // Index k of a row's LSB-first group (cactus_x86.cpp:24-43), any bits in 1..4.
@@ -294,68 +313,84 @@ __global__ __launch_bounds__(256) void cq4_gemv_kernel(Cq4View w, const float* _
 
 // MFMA form for 4-bit LSB-packed indices (the packing of cactus_x86.cpp:24-43 with
 // bits = 4: column n's K/2 bytes are contiguous, index k in the low nibble of byte
-// k/2 when k is even), a group size that is a multiple of 32 and M >= 32. The
-// weight bytes then have exactly the int4 GEMM's layout, and the int4 wide
-// kernel's design carries over: v_mfma_f32_16x16x4_f32, lane (j, q) feeding K slot
-// q with k = 8q + t at step t, so its B operands are the 8 indices of word q of a
-// 32-value sub-group. A workgroup owns a 64 x 64 tile (2 x 2 wavefronts of 32 x 32;
-// 256 workgroups at M = N = 1024) and stages two sub-groups at a time (K % 64 == 0)
-// through two LDS buffers, one barrier per pair:
-// the code-basis activations (64 rows x 32 floats) copied global -> LDS by
-// global_load_lds_dwordx4 as full 128-byte rows, XOR-swizzled within 256-byte row
-// pairs so MFMA-operand reads hit 16 bank groups; the weights decoded once per
-// workgroup (each thread one 32-bit word: 8 codebook lookups in LDS) into fp32 in
-// the MFMA B layout. The MFMA sums each 32-value sub-group in fp32, and the sub-group
-// sum times its group's norm is accumulated in float64 (exact product); C is rounded
-// to fp16 once. (The reference sums a whole group in fp32 before the norm,
-// cactus_x86.cpp:214-226: over K = 1024 that leaves errors of ~1.5e-5 near zero
-// outputs, beyond the fp16 rounding this path is held to; 32-value sums folded in
-// float64 stay under 6.2e-6 in an emulation of 131,072 outputs.)
+// k/2 when k is even), a group size that is a multiple of 32, K % 64 == 0 and
+// M >= 32. The weight bytes then have exactly the int4 GEMM's layout, and the int4
+// wide kernel's design carries over: v_mfma_f32_16x16x32_bf16 on exact bf16 limbs.
+//   - The transform stores each code-basis activation (an fp32 value) as three
+//     bf16 limbs (split_bf16_limbs: b0 + b1 + b2 == A' exactly), laid out
+//     [M][K/64][3][64], so no fp32 copy of A' is written.
+//   - A codebook value (fp16, 11 significant bits) is the sum of two bf16 limbs:
+//     its top 8 significant bits and the remaining 3 (the fp16 exponent range lies
+//     inside bf16's). The 16 entries sit in LDS as (high | low << 16) pairs.
+//   - So every limb product is exact in fp32, and six MFMAs per 32-value sub-group
+//     (3 activation limbs x 2 codebook limbs, smallest first) sum the sub-group's
+//     products in fp32, as the fp32 MFMA form did with eight 16x16x4 MFMAs at
+//     sixteen times the matrix-core cycles each.
+// Lane (j, q) of a 16x16x32 MFMA holds A[row j][k = 8q .. 8q+7] and B[k = 8q ..
+// 8q+7][column j], so its B operands are the 8 indices of word q of a sub-group.
+// A workgroup owns a 64 x 64 tile (2 x 2 wavefronts of 32 x 32; 256 workgroups at
+// M = N = 1024) and stages 64 values of K (two sub-groups) at a time through two
+// LDS buffers, one barrier per stage: the activation limbs (3 x 64 rows x 64
+// values) copied global -> LDS by global_load_lds_dwordx4 as full 128-byte rows,
+// XOR-swizzled within 256-byte row pairs so MFMA-operand reads hit 16 bank groups;
+// the weights decoded once per workgroup (each thread one 32-bit word per
+// sub-group: 8 table lookups in LDS, 8 byte permutes) into both codebook limbs in
+// the MFMA B layout. Each sub-group sum times its group's norm is accumulated in
+// float64 (exact product); C is rounded to fp16 once. (The reference sums a whole
+// group in fp32 before the norm, cactus_x86.cpp:214-226: over K = 1024 that leaves
+// errors of ~1.5e-5 near zero outputs, beyond the fp16 rounding this path is held
+// to; 32-value sums folded in float64 stay under 6.2e-6 in an emulation of
+// 131,072 outputs.)
 constexpr uint32_t kCq4MfmaMinRows = 32;
 constexpr int kCq4Tile = 64;
-constexpr int kCq4SubPerStage = 2;  // 32-value sub-groups staged per barrier
+constexpr int kCq4Limbs = 3;
 
 struct Cq4MfmaStage {
-    // per sub-group u: row r's 16-byte chunk c (k = 32 s + 4 c .. +3) at f32x4 index
-    // (r >> 1) * 16 + 8 (r & 1) + (c ^ ((r >> 1) & 7)) of a[u]
-    f32x4_t a[kCq4SubPerStage][8 * 64];
-    // per sub-group u: slot (nh * 2 + tn) * 2 + h, lane (j, q): codebook values of
-    // k = 32 s + 8 q + 4 h .. +3 of column 32 nh + 16 tn + j
-    f32x4_t b[kCq4SubPerStage][8][64];
+    // activation limb li, 8-row block, lane slot: row r's 16-byte chunk c (k = 64 t + 8 c .. +7)
+    // at u32x4 index (r >> 1) * 16 + 8 (r & 1) + (c ^ ((r >> 1) & 7)) of a[li]
+    u32x4 a[kCq4Limbs][8][64];
+    // sub-group u, codebook limb (0 high, 1 low), 16-column tile, lane (j, q): the limbs of the
+    // codebook values of k = 64 t + 32 u + 8 q .. +7 of column 16 tile + j
+    u32x4 b[2][2][4][64];
 };
 
-__global__ __launch_bounds__(256) void cq4_gemm_mfma_kernel(Cq4View w, const float* __restrict__ ap,
+__global__ __launch_bounds__(256) void cq4_gemm_mfma_kernel(Cq4View w, const uint16_t* __restrict__ xs,
                                                            uint16_t* __restrict__ c, uint32_t M, uint32_t gs,
                                                            uint32_t ng, uint32_t tiles_m) {
     __shared__ Cq4MfmaStage stage[2];
-    __shared__ float lut[16];
+    __shared__ uint32_t lut[16];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wid & 1, wn = wid >> 1;
     const int j = lane & 15, q = lane >> 4;
     const int K = static_cast<int>(w.K), N = static_cast<int>(w.N), Mi = static_cast<int>(M);
-    const int T = K / (32 * kCq4SubPerStage);      // stages (K % 64 == 0)
-    const int spg = static_cast<int>(gs) >> 5;     // sub-groups per norm group
+    const int T = K / 64;                       // stages (K % 64 == 0)
+    const int spg = static_cast<int>(gs) >> 5;  // sub-groups per norm group
     const int mt0 = static_cast<int>(blockIdx.x % tiles_m) * kCq4Tile;
     const int nt0 = static_cast<int>(blockIdx.x / tiles_m) * kCq4Tile;
     const int m0 = mt0 + 32 * wm, n0 = nt0 + 32 * wn;
-    if (tid < 16) lut[tid] = half_bits_to_float(w.codebook[tid]);
+    if (tid < 16) {
+        const float v = half_bits_to_float(w.codebook[tid]);
+        const uint32_t hi = __float_as_uint(v) & 0xFFFF0000u;
+        const float lo = v - __uint_as_float(hi);  // exact, at most 3 significant bits
+        lut[tid] = (hi >> 16) | (__float_as_uint(lo) & 0xFFFF0000u);
+    }
 
-    // A copies: per sub-group, instructions 2 wid and 2 wid + 1, each 8 full rows.
-    const float* asrc[2];
+    // Activation-limb copies of this wavefront: 8-row blocks 2 wid and 2 wid + 1, three limbs each.
+    const uint16_t* asrc[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const int ins = 2 * wid + i;
-        const int pair = 4 * ins + (lane >> 4);
+        const int blk = 2 * wid + i;
+        const int pair = 4 * blk + (lane >> 4);
         const int row_t = 2 * pair + ((lane >> 3) & 1);
-        asrc[i] = ap + static_cast<size_t>(min(mt0 + row_t, Mi - 1)) * K + 4 * ((lane & 7) ^ (pair & 7));
+        asrc[i] = xs + static_cast<size_t>(min(mt0 + row_t, Mi - 1)) * T * (kCq4Limbs * 64) +
+                  8 * ((lane & 7) ^ (pair & 7));
     }
     // B: thread -> tile column bc, word bw of each sub-group's 16 bytes.
     const int bc = tid >> 2, bw = tid & 3;
     const uint32_t* bsrc =
         reinterpret_cast<const uint32_t*>(w.packed + static_cast<size_t>(min(nt0 + bc, N - 1)) * (K >> 1)) + bw;
-    const int bslot = ((bc >> 5) * 2 + ((bc >> 4) & 1)) * 2;
     const int blane = (bc & 15) + 16 * bw;
     const uint16_t* nrm[2];
 #pragma unroll
@@ -363,24 +398,30 @@ __global__ __launch_bounds__(256) void cq4_gemm_mfma_kernel(Cq4View w, const flo
 
     auto issue_a = [&](int t, int st) {
 #pragma unroll
-        for (int u = 0; u < kCq4SubPerStage; ++u)
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-                __builtin_amdgcn_global_load_lds(asrc[i] + (kCq4SubPerStage * t + u) * 32,
-                                                 &stage[st].a[u][(2 * wid + i) * 64], 16, 0, 0);
+            for (int li = 0; li < kCq4Limbs; ++li)  // 1 KiB = 8 rows of one limb
+                __builtin_amdgcn_global_load_lds(asrc[i] + static_cast<size_t>(t) * (kCq4Limbs * 64) + li * 64,
+                                                 &stage[st].a[li][2 * wid + i][0], 16, 0, 0);
     };
-    auto load_b = [&](int t, uint32_t (&wd)[kCq4SubPerStage]) {
+    auto load_b = [&](int t, uint32_t (&wd)[2]) {
 #pragma unroll
-        for (int u = 0; u < kCq4SubPerStage; ++u) wd[u] = bsrc[4 * (kCq4SubPerStage * t + u)];
+        for (int u = 0; u < 2; ++u) wd[u] = bsrc[4 * (2 * t + u)];
     };
-    auto write_b = [&](const uint32_t (&wd)[kCq4SubPerStage], int st) {
+    auto write_b = [&](const uint32_t (&wd)[2], int st) {
 #pragma unroll
-        for (int u = 0; u < kCq4SubPerStage; ++u) {
-            float f[8];
+        for (int u = 0; u < 2; ++u) {
+            uint32_t e[8];
 #pragma unroll
-            for (int t = 0; t < 8; ++t) f[t] = lut[(wd[u] >> (4 * t)) & 0xFu];
-            stage[st].b[u][bslot][blane] = f32x4_t{f[0], f[1], f[2], f[3]};
-            stage[st].b[u][bslot + 1][blane] = f32x4_t{f[4], f[5], f[6], f[7]};
+            for (int t = 0; t < 8; ++t) e[t] = lut[(wd[u] >> (4 * t)) & 0xFu];
+            u32x4 hi, lo;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                hi[i] = __builtin_amdgcn_perm(e[2 * i + 1], e[2 * i], 0x05040100u);  // low halves
+                lo[i] = __builtin_amdgcn_perm(e[2 * i + 1], e[2 * i], 0x07060302u);  // high halves
+            }
+            stage[st].b[u][0][bc >> 4][blane] = hi;
+            stage[st].b[u][1][bc >> 4][blane] = lo;
         }
     };
 
@@ -395,7 +436,7 @@ __global__ __launch_bounds__(256) void cq4_gemm_mfma_kernel(Cq4View w, const flo
     __syncthreads();  // the codebook is in LDS
     {
         issue_a(0, 0);
-        uint32_t wd[kCq4SubPerStage];
+        uint32_t wd[2];
         load_b(0, wd);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         write_b(wd, 0);
@@ -404,35 +445,40 @@ __global__ __launch_bounds__(256) void cq4_gemm_mfma_kernel(Cq4View w, const flo
     for (int t = 0; t < T; ++t) {
         const int st = t & 1;
         const bool more = t + 1 < T;  // uniform
-        uint32_t wdn[kCq4SubPerStage] = {};
+        uint32_t wdn[2] = {};
         if (more) {
             issue_a(t + 1, st ^ 1);
             load_b(t + 1, wdn);
         }
 #pragma unroll
-        for (int u = 0; u < kCq4SubPerStage; ++u) {
+        for (int u = 0; u < 2; ++u) {
+            bf16x8 bh[2], bl[2];
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn) {
+                bh[tn] = __builtin_bit_cast(bf16x8, stage[st].b[u][0][wn * 2 + tn][lane]);
+                bl[tn] = __builtin_bit_cast(bf16x8, stage[st].b[u][1][wn * 2 + tn][lane]);
+            }
             f32x4_t P[2][2];
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                f32x4_t av[2], bv[2];
+            for (int tm = 0; tm < 2; ++tm) {
+                const int row_t = 32 * wm + 16 * tm + j;
+                const int pr = row_t >> 1;
+                const int idx = pr * 16 + 8 * (row_t & 1) + ((4 * u + q) ^ (pr & 7));
+                bf16x8 av[kCq4Limbs];
 #pragma unroll
-                for (int tm = 0; tm < 2; ++tm) {
-                    const int row_t = 32 * wm + 16 * tm + j;
-                    const int pr = row_t >> 1;
-                    av[tm] = stage[st].a[u][pr * 16 + 8 * (row_t & 1) + ((2 * q + h) ^ (pr & 7))];
+                for (int li = 0; li < kCq4Limbs; ++li)
+                    av[li] = __builtin_bit_cast(bf16x8, (&stage[st].a[li][0][0])[idx]);
+#pragma unroll
+                for (int tn = 0; tn < 2; ++tn) {
+                    f32x4_t r = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[2], bl[tn], zero, 0, 0, 0);
+                    r = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[1], bl[tn], r, 0, 0, 0);
+                    r = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[2], bh[tn], r, 0, 0, 0);
+                    r = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[0], bl[tn], r, 0, 0, 0);
+                    r = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[1], bh[tn], r, 0, 0, 0);
+                    P[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[0], bh[tn], r, 0, 0, 0);
                 }
-#pragma unroll
-                for (int tn = 0; tn < 2; ++tn) bv[tn] = stage[st].b[u][(wn * 2 + tn) * 2 + h][lane];
-#pragma unroll
-                for (int k4 = 0; k4 < 4; ++k4)
-#pragma unroll
-                    for (int tm = 0; tm < 2; ++tm)
-#pragma unroll
-                        for (int tn = 0; tn < 2; ++tn)
-                            P[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x4f32(
-                                av[tm][k4], bv[tn][k4], (h == 0 && k4 == 0) ? zero : P[tm][tn], 0, 0, 0);
             }
-            const int g = (kCq4SubPerStage * t + u) / spg;
+            const int g = (2 * t + u) / spg;
 #pragma unroll
             for (int tn = 0; tn < 2; ++tn) {
                 const double nv = static_cast<double>(half_bits_to_float(nrm[tn][g]));
@@ -462,6 +508,13 @@ __global__ __launch_bounds__(256) void cq4_gemm_mfma_kernel(Cq4View w, const flo
         }
 }
 
+bool cq4_uses_mfma(const Cq4View& w, uint32_t m) {
+    const bool orth = (w.flags & kCq4FlagOrthogonal) != 0;
+    const uint32_t gs = orth ? w.K : w.group_size;
+    const bool inter = (w.flags & kCq4FlagInterleaved4Row) != 0;
+    return m >= kCq4MfmaMinRows && w.bits == 4 && !inter && gs % 32 == 0 && w.K % 64 == 0;
+}
+
 template <int ROWS>
 hipError_t launch_gemm(const Cq4View& w, const float* ap, uint16_t* c, uint32_t m, uint32_t gs, uint32_t ng,
                        hipStream_t stream) {
@@ -478,48 +531,58 @@ hipError_t launch_gemm(const Cq4View& w, const float* ap, uint16_t* c, uint32_t 
 
 }  // namespace
 
-hipError_t launch_cq4_matmul(const Cq4View& w, const uint16_t* a, uint32_t m, uint16_t* c, float* workspace,
+size_t cq4_workspace_bytes(const Cq4View& w, uint32_t m) {
+    const size_t values = static_cast<size_t>(m) * w.K;  // K % 64 == 0 on the MFMA path: no padding
+    return cq4_uses_mfma(w, m) ? values * 3 * sizeof(uint16_t) : values * sizeof(float);
+}
+
+hipError_t launch_cq4_matmul(const Cq4View& w, const uint16_t* a, uint32_t m, uint16_t* c, void* workspace,
                              hipStream_t stream) {
+    // The transform writes the code-basis activations as fp32 rows, or, for the MFMA GEMM, directly as
+    // their bf16 limbs.
+    const bool mfma = cq4_uses_mfma(w, m);
+    float* ap = mfma ? nullptr : static_cast<float*>(workspace);
+    uint16_t* xs = mfma ? static_cast<uint16_t*>(workspace) : nullptr;
     const bool orth = (w.flags & kCq4FlagOrthogonal) != 0;
     const uint32_t gs = orth ? w.K : w.group_size, ng = orth ? 1 : w.num_groups;
     if (orth) {
         hipLaunchKernelGGL(cq4_transform_orthogonal_kernel, dim3((w.K + 255) / 256, m), dim3(256), 0, stream, w, a,
-                           workspace);
+                           ap, xs);
     } else if (w.group_size == 64 || w.group_size == 128 || w.group_size == 256) {
         const uint32_t pairs = m * w.num_groups;
         const dim3 grid((pairs + 3) / 4);
         if (w.group_size == 64)
-            hipLaunchKernelGGL(cq4_transform_hadamard_wave_kernel<1>, grid, dim3(256), 0, stream, w, a, workspace, pairs);
+            hipLaunchKernelGGL(cq4_transform_hadamard_wave_kernel<1>, grid, dim3(256), 0, stream, w, a, ap, xs, pairs);
         else if (w.group_size == 128)
-            hipLaunchKernelGGL(cq4_transform_hadamard_wave_kernel<2>, grid, dim3(256), 0, stream, w, a, workspace, pairs);
+            hipLaunchKernelGGL(cq4_transform_hadamard_wave_kernel<2>, grid, dim3(256), 0, stream, w, a, ap, xs, pairs);
         else
-            hipLaunchKernelGGL(cq4_transform_hadamard_wave_kernel<4>, grid, dim3(256), 0, stream, w, a, workspace, pairs);
+            hipLaunchKernelGGL(cq4_transform_hadamard_wave_kernel<4>, grid, dim3(256), 0, stream, w, a, ap, xs, pairs);
     } else {
         // group_size / 2 threads (one for a group of 1, whose transform is the identity)
         hipLaunchKernelGGL(cq4_transform_hadamard_kernel, dim3(w.num_groups, m), dim3(w.group_size > 1 ? w.group_size / 2 : 1),
-                           0, stream, w, a, workspace);
+                           0, stream, w, a, ap, xs);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const bool inter = (w.flags & kCq4FlagInterleaved4Row) != 0;
-    if (m >= kCq4MfmaMinRows && w.bits == 4 && !inter && gs % 32 == 0 && w.K % (32 * kCq4SubPerStage) == 0) {
+    if (mfma) {
         const uint32_t tiles_m = (m + kCq4Tile - 1) / kCq4Tile, tiles_n = (w.N + kCq4Tile - 1) / kCq4Tile;
-        hipLaunchKernelGGL(cq4_gemm_mfma_kernel, dim3(tiles_m * tiles_n), dim3(256), 0, stream, w, workspace, c, m,
-                           gs, ng, tiles_m);
+        hipLaunchKernelGGL(cq4_gemm_mfma_kernel, dim3(tiles_m * tiles_n), dim3(256), 0, stream, w, xs, c, m, gs, ng,
+                           tiles_m);
         return hipGetLastError();
     }
     if (m <= 4 && w.bits == 4 && gs % 8 == 0) {
         const dim3 grid((w.N + 3) / 4);
         if (m == 1) {
-            if (inter) hipLaunchKernelGGL((cq4_gemv_kernel<1, true>), grid, dim3(256), 0, stream, w, workspace, c, m, gs, ng);
-            else hipLaunchKernelGGL((cq4_gemv_kernel<1, false>), grid, dim3(256), 0, stream, w, workspace, c, m, gs, ng);
+            if (inter) hipLaunchKernelGGL((cq4_gemv_kernel<1, true>), grid, dim3(256), 0, stream, w, ap, c, m, gs, ng);
+            else hipLaunchKernelGGL((cq4_gemv_kernel<1, false>), grid, dim3(256), 0, stream, w, ap, c, m, gs, ng);
         } else {
-            if (inter) hipLaunchKernelGGL((cq4_gemv_kernel<4, true>), grid, dim3(256), 0, stream, w, workspace, c, m, gs, ng);
-            else hipLaunchKernelGGL((cq4_gemv_kernel<4, false>), grid, dim3(256), 0, stream, w, workspace, c, m, gs, ng);
+            if (inter) hipLaunchKernelGGL((cq4_gemv_kernel<4, true>), grid, dim3(256), 0, stream, w, ap, c, m, gs, ng);
+            else hipLaunchKernelGGL((cq4_gemv_kernel<4, false>), grid, dim3(256), 0, stream, w, ap, c, m, gs, ng);
         }
         return hipGetLastError();
     }
-    return m >= 4 ? launch_gemm<4>(w, workspace, c, m, gs, ng, stream) : launch_gemm<1>(w, workspace, c, m, gs, ng, stream);
+    return m >= 4 ? launch_gemm<4>(w, ap, c, m, gs, ng, stream) : launch_gemm<1>(w, ap, c, m, gs, ng, stream);
 }
 
 }  // namespace spaceslug

@@ -26,9 +26,13 @@ struct Cq4View {
     const uint16_t* rotation;
 };
 
-// C[m][N] (fp16) = transform(A[m][K] fp16) x decode(W). `workspace` holds m * K floats
-// (the code-basis activations). Arguments are validated by the caller.
-hipError_t launch_cq4_matmul(const Cq4View& w, const uint16_t* a, uint32_t m, uint16_t* c, float* workspace,
+// Device bytes launch_cq4_matmul needs for m rows: the code-basis activations, as m * K floats,
+// or on the MFMA path as their bf16 limbs (6 * m * K bytes).
+size_t cq4_workspace_bytes(const Cq4View& w, uint32_t m);
+
+// C[m][N] (fp16) = transform(A[m][K] fp16) x decode(W). `workspace` holds
+// cq4_workspace_bytes(w, m) bytes, 256-byte aligned. Arguments are validated by the caller.
+hipError_t launch_cq4_matmul(const Cq4View& w, const uint16_t* a, uint32_t m, uint16_t* c, void* workspace,
                              hipStream_t stream);
 
 }  // namespace spaceslug

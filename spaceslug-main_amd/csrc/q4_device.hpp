@@ -59,6 +59,20 @@ constexpr float kSixteenthsUnit = 16.0f;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
+// x == b0 + b1 + b2 exactly, each a bf16 (bit patterns in b[0..2], low 16 bits): b0 is x
+// truncated to its top 8 significant bits (truncation, so nothing rounds past the fp32
+// range), b1 is x - b0 truncated the same way, and b2 = x - b0 - b1 has at most 8 significant
+// bits. Both subtractions are exact in fp32, subnormals included.
+__device__ __forceinline__ void split_bf16_limbs(float x, uint32_t (&b)[3]) {
+    const float b0 = __uint_as_float(__float_as_uint(x) & 0xFFFF0000u);
+    const float r1 = x - b0;
+    const float b1 = __uint_as_float(__float_as_uint(r1) & 0xFFFF0000u);
+    const float r2 = r1 - b1;
+    b[0] = __float_as_uint(b0) >> 16;
+    b[1] = __float_as_uint(b1) >> 16;
+    b[2] = __float_as_uint(r2) >> 16;
+}
+
 // The 8 nibbles of w as bf16 v / 16, packed in element order (element t in the
 // low half of word t/2 when t is even, the high half when odd). v / 16 has at
 // most three significant bits, so the high half of its fp32 form is the exact

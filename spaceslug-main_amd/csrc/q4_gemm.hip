@@ -229,11 +229,8 @@ constexpr int kLimbs = 3;
 
 // x (fp32, M x K) -> x limbs (bf16, [M][KB][3][64] with KB = ceil(K / 64), rows
 // zero-padded to KB * 64 values) for q4_gemm_wide_kernel. Each value is split
-// exactly: b0 = x truncated to bf16 (the top 8 significant bits, so never
-// rounded up past the fp32 range), b1 = (x - b0) truncated the same way, and
-// b2 = x - b0 - b1, which has at most 8 significant bits and is exact in bf16;
-// both subtractions are exact in fp32. So b0 + b1 + b2 == x for every finite x,
-// and a product of a limb with a bf16 weight v/16 is exact in fp32.
+// exactly (split_bf16_limbs: b0 + b1 + b2 == x for every finite x), so a product
+// of a limb with a bf16 weight v/16 is exact in fp32.
 // One thread per 8 consecutive values of a row: two 16-byte loads, three
 // 16-byte stores (one per limb), coalesced along the row.
 __global__ __launch_bounds__(256) void split_x_kernel(const float* __restrict__ x, uint16_t* __restrict__ xs,
@@ -261,19 +258,11 @@ __global__ __launch_bounds__(256) void split_x_kernel(const float* __restrict__ 
     u32x4 limb[kLimbs];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-        uint32_t bits[kLimbs][2];
+        uint32_t lo[kLimbs], hi[kLimbs];
+        split_bf16_limbs(v[2 * t], lo);
+        split_bf16_limbs(v[2 * t + 1], hi);
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const float b0 = __uint_as_float(__float_as_uint(v[2 * t + e]) & 0xFFFF0000u);
-            const float r1 = v[2 * t + e] - b0;
-            const float b1 = __uint_as_float(__float_as_uint(r1) & 0xFFFF0000u);
-            const float r2 = r1 - b1;
-            bits[0][e] = __float_as_uint(b0) >> 16;
-            bits[1][e] = __float_as_uint(b1) >> 16;
-            bits[2][e] = __float_as_uint(r2) >> 16;
-        }
-#pragma unroll
-        for (int li = 0; li < kLimbs; ++li) limb[li][t] = bits[li][0] | (bits[li][1] << 16);
+        for (int li = 0; li < kLimbs; ++li) limb[li][t] = lo[li] | (hi[li] << 16);
     }
     uint16_t* dst = xs + (static_cast<size_t>(row) * KB + kb) * (kLimbs * 64) + c * 8;
 #pragma unroll
@@ -771,12 +760,20 @@ constexpr int kWideWaves = 4;
 
 size_t align_up(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
-// Bytes of the wide kernel's x limbs: M rows x ceil(K / 64) stages x 3 limbs x 64 bf16.
-size_t wide_limb_bytes(uint32_t m, uint32_t k) {
+
+}  // namespace
+
+size_t split_x_bf16_bytes(uint32_t m, uint32_t k) {
     return static_cast<size_t>(m) * ((k / kGroup + 1) / 2) * kLimbs * 64 * sizeof(uint16_t);
 }
 
-}  // namespace
+hipError_t launch_split_x_bf16(const float* x, uint16_t* xs, uint32_t m, uint32_t k, hipStream_t stream) {
+    const int KB = static_cast<int>((k / kGroup + 1) / 2);
+    const size_t chunks = static_cast<size_t>(m) * KB * 8;
+    hipLaunchKernelGGL(split_x_kernel, dim3(static_cast<unsigned>((chunks + 255) / 256)), dim3(256), 0, stream, x, xs,
+                       static_cast<int>(m), static_cast<int>(k), KB);
+    return hipGetLastError();
+}
 
 Q4Plan plan_q4gemm(const DeviceInfo& dev, uint32_t m, uint32_t n, uint32_t k, uint32_t rank) {
     Q4Plan plan{Q4Plan::kGemv, 1, 0, 0};
@@ -821,7 +818,7 @@ Q4Plan plan_q4gemm(const DeviceInfo& dev, uint32_t m, uint32_t n, uint32_t k, ui
     splits = (units + per_split - 1) / per_split;
     plan.splits = splits;
     size_t bytes = lora_bytes;
-    if (plan.kind == Q4Plan::kWide) bytes += align_up(wide_limb_bytes(m, k));  // x limbs
+    if (plan.kind == Q4Plan::kWide) bytes += align_up(split_x_bf16_bytes(m, k));  // x limbs
     if (splits > 1) bytes += align_up(static_cast<size_t>(splits) * m * n * sizeof(float));
     plan.workspace_bytes = bytes;
     return plan;
@@ -884,10 +881,7 @@ hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float*
         const int KB = static_cast<int>((k / kGroup + 1) / 2);
         const int stages_per_split = (KB + plan.splits - 1) / plan.splits;
         uint16_t* xs = reinterpret_cast<uint16_t*>(wsp);
-        const size_t chunks = static_cast<size_t>(m) * KB * 8;
-        hipLaunchKernelGGL(split_x_kernel, dim3(static_cast<unsigned>((chunks + 255) / 256)), dim3(256), 0, stream, x,
-                           xs, static_cast<int>(m), static_cast<int>(k), KB);
-        e = hipGetLastError();
+        e = launch_split_x_bf16(x, xs, m, k, stream);
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL(q4_gemm_wide_kernel, dim3(tiles_m * tiles_n, plan.splits), dim3(64 * kWideWaves), 0,
                            stream, xs, reinterpret_cast<const uint32_t*>(w_packed), w_scales, out, static_cast<int>(m),

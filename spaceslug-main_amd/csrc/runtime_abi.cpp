@@ -539,7 +539,8 @@ int spaceslug_cq4_matmul(const spaceslug_cq4_matrix* w, const uint16_t* a, uint3
         (void)current_device();
         const size_t a_bytes = static_cast<size_t>(m) * w->K * 2, c_bytes = static_cast<size_t>(m) * w->N * 2;
         const bool has_scale = w->input_scale_recip || w->input_scale;
-        StagingArena arena({a_bytes, c_bytes, static_cast<size_t>(m) * w->K * sizeof(float), sz.codebook,
+        const spaceslug::Cq4View shape{w->bits, w->K, w->N, w->group_size, w->num_groups, w->flags};
+        StagingArena arena({a_bytes, c_bytes, spaceslug::cq4_workspace_bytes(shape, m), sz.codebook,
                             has_scale ? sz.scale : 0, sz.norms, sz.packed, w->left_signs ? sz.signs : 0,
                             w->right_signs ? sz.signs : 0, w->permutation ? sz.perm : 0, sz.rotation});
         auto up = [&](size_t slot, const void* host, size_t bytes) -> void* {
@@ -559,7 +560,7 @@ int spaceslug_cq4_matmul(const spaceslug_cq4_matrix* w, const uint16_t* a, uint3
         if (w->input_scale_recip) v.input_scale_recip = static_cast<const uint16_t*>(up(4, w->input_scale_recip, sz.scale));
         else if (w->input_scale) v.input_scale = static_cast<const uint16_t*>(up(4, w->input_scale, sz.scale));
         const uint16_t* da = static_cast<const uint16_t*>(up(0, a, a_bytes));
-        check(spaceslug::launch_cq4_matmul(v, da, m, arena.slice<uint16_t>(1), arena.slice<float>(2), nullptr),
+        check(spaceslug::launch_cq4_matmul(v, da, m, arena.slice<uint16_t>(1), arena.slice<void>(2), nullptr),
               "cq4 launch");
         check(hipMemcpy(c, arena.slice<uint16_t>(1), c_bytes, hipMemcpyDeviceToHost), "hipMemcpy (cq4 output)");
         return ok();
@@ -589,7 +590,7 @@ int spaceslug_cq4_matmul_device(const spaceslug_cq4_matrix* w, const uint16_t* d
         DeviceState& dev = current_device();
         const hipStream_t st = static_cast<hipStream_t>(stream);
         std::lock_guard<std::mutex> lock(g_device_mutex);
-        float* ws = static_cast<float*>(device_workspace(dev, static_cast<size_t>(m) * w->K * sizeof(float)));
+        void* ws = device_workspace(dev, spaceslug::cq4_workspace_bytes(v, m));
         if (!dev.ws_done) check(hipEventCreateWithFlags(&dev.ws_done, hipEventDisableTiming), "hipEventCreateWithFlags");
         if (dev.ws_used && dev.ws_stream != st) check(hipStreamWaitEvent(st, dev.ws_done, 0), "hipStreamWaitEvent");
         check(spaceslug::launch_cq4_matmul(v, d_a, m, d_c, ws, st), "cq4 launch");
