@@ -317,8 +317,8 @@ __global__ __launch_bounds__(256) void cq4_gemv_kernel(Cq4View w, const float* _
 // M >= 32. The weight bytes then have exactly the int4 GEMM's layout, and the int4
 // wide kernel's design carries over: v_mfma_f32_16x16x32_bf16 on exact bf16 limbs.
 //   - The transform stores each code-basis activation (an fp32 value) as three
-//     bf16 limbs (split_bf16_limbs: b0 + b1 + b2 == A' exactly), laid out
-//     [M][K/64][3][64], so no fp32 copy of A' is written.
+//     bf16 limbs (split_bf16_limbs: b0 + b1 + b2 == A' for |A'| >= 2^-110, within
+//     2^-133 below), laid out [M][K/64][3][64], so no fp32 copy of A' is written.
 //   - A codebook value (fp16, 11 significant bits) is the sum of two bf16 limbs:
 //     its top 8 significant bits and the remaining 3 (the fp16 exponent range lies
 //     inside bf16's). The 16 entries sit in LDS as (high | low << 16) pairs.

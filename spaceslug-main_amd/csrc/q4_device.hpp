@@ -59,10 +59,12 @@ constexpr float kSixteenthsUnit = 16.0f;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-// x == b0 + b1 + b2 exactly, each a bf16 (bit patterns in b[0..2], low 16 bits): b0 is x
-// truncated to its top 8 significant bits (truncation, so nothing rounds past the fp32
-// range), b1 is x - b0 truncated the same way, and b2 = x - b0 - b1 has at most 8 significant
-// bits. Both subtractions are exact in fp32, subnormals included.
+// x as three bf16 limbs (bit patterns in b[0..2], low 16 bits): b0 is x truncated to its top
+// 8 significant bits (truncation, so nothing rounds past the fp32 range), b1 is x - b0
+// truncated the same way, and b2 = x - b0 - b1 has at most 8 significant bits. Both
+// subtractions are exact in fp32, so b0 + b1 + b2 == x whenever x's lowest significant bit is
+// at least 2^-133 (bf16's subnormal resolution): every |x| >= 2^-110, and zero. Below that
+// the limbs drop at most 2^-133 of x.
 __device__ __forceinline__ void split_bf16_limbs(float x, uint32_t (&b)[3]) {
     const float b0 = __uint_as_float(__float_as_uint(x) & 0xFFFF0000u);
     const float r1 = x - b0;

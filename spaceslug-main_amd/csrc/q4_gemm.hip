@@ -228,9 +228,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void q4_gemm_mfma_kernel(
 constexpr int kLimbs = 3;
 
 // x (fp32, M x K) -> x limbs (bf16, [M][KB][3][64] with KB = ceil(K / 64), rows
-// zero-padded to KB * 64 values) for q4_gemm_wide_kernel. Each value is split
-// exactly (split_bf16_limbs: b0 + b1 + b2 == x for every finite x), so a product
-// of a limb with a bf16 weight v/16 is exact in fp32.
+// zero-padded to KB * 64 values) for q4_gemm_wide_kernel. Each value is split by
+// split_bf16_limbs (b0 + b1 + b2 == x for |x| >= 2^-110, within 2^-133 below), and a
+// product of a limb with a bf16 weight v/16 is exact in fp32.
 // One thread per 8 consecutive values of a row: two 16-byte loads, three
 // 16-byte stores (one per limb), coalesced along the row.
 __global__ __launch_bounds__(256) void split_x_kernel(const float* __restrict__ x, uint16_t* __restrict__ xs,
