@@ -343,7 +343,8 @@ int spaceslug_sgemm(const float* a, const float* b, float* c, uint32_t m, uint32
 
 const char* spaceslug_q4gemm_capability(void) {
     return "q4gemm-hip-gfx950 group=32 layout=n-major-lsb-nibble decode=gemv(m<=4; m=1,k<=4096: int4-digit dot8) "
-           "prefill=mfma-f32-16x16x4 accumulate=f32-group+f64 lora=fused-epilogue(rank<=64) "
+           "gemm=mfma(m<=32: f32-16x16x4; m>32: bf16-16x16x32 on 3 exact x limbs) accumulate=f32-group+f64 "
+           "lora=fused-epilogue(rank<=64) "
            "chain=fixed_shape_retained_hip_graph_replay";
 }
 
