@@ -15,10 +15,11 @@
 //     to v / 16 (v_cvt_off_f32_i4, exact; the factor 16 joins the scale);
 //   - every product x * v / 16 is exact in fp32; the MFMA accumulates
 //     P = sum x * v / 16 over one group in fp32 from zero, and the group is
-//     folded into a float64 accumulator as acc += (double)(16 s) * P. Scale
-//     application moves out of the inner loop, and the long K sum is carried in
-//     double, which keeps the max relative error against the double-precision
-//     reference well under 1e-5 at K = 4096;
+//     folded as 16 s * P: straight into a float64 accumulator in the small-M
+//     kernels, into an fp32 accumulator that is added into float64 every 8 groups
+//     in the wide kernel. Scale application moves out of the inner loop, and the
+//     long K sum is carried in double, which keeps the max relative error against
+//     the double-precision reference well under 1e-5 at K = 4096;
 //   - large grids are XCD-aware: workgroup ids are remapped so each of the 8
 //     XCDs (one L2 each) walks a contiguous band of output tiles, sharing A
 //     rows and weight columns within its L2;
@@ -274,9 +275,14 @@ __global__ __launch_bounds__(256) void split_x_kernel(const float* __restrict__ 
 // per SIMD. The matrix instruction is v_mfma_f32_16x16x32_bf16, fed with x as
 // three exact bf16 limbs (split_x_kernel) and the weights as bf16 v/16 (exact):
 // every product is exact in fp32, each 32-value group's sum P = sum x * v/16 is
-// accumulated in fp32 by three chained MFMAs (smallest limb first), and the
-// group is folded into a float64 accumulator as acc += (double)(16 s) * P, as on
-// the other GEMM paths. One such MFMA (16 x 16 x 32) does the work of eight
+// accumulated in fp32 by three chained MFMAs (smallest limb first). The group is
+// folded into an fp32 accumulator as acc32 += 16 s * P, and every 4 stages (8
+// groups) acc32 is added into the float64 accumulator: one fp32 FMA per output and
+// group instead of a convert and a float64 FMA, and 64 fewer live registers
+// between flushes. Against the per-group float64 fold: 1.24 against 1.34 ms at
+// M=2048, K=4096, N=14336 (same box); the measured max relative error stays
+// under 1e-5 (an emulation of this order at 2.9e7 outputs: 4.1-4.8e-6 against
+// 3.8-4.0e-6 for the per-group fold). One such MFMA (16 x 16 x 32) does the work of eight
 // fp32 16x16x4 MFMAs at a sixteenth of their matrix-core cycles each, so three
 // of them cost under a fifth of the fp32 form.
 // Lane (j = l%16, q = l/16) of a 16x16x32 MFMA holds A[row j][k = 8q .. 8q+7] and
@@ -298,7 +304,7 @@ __global__ __launch_bounds__(256) void split_x_kernel(const float* __restrict__ 
 // fold are skipped (a wavefront-uniform branch). Against the same tile on
 // v_mfma_f32_16x16x4_f32 with x staged as fp32 (the previous product kernel):
 // 1.34 against 2.28-2.32 ms at M=2048, K=4096, N=14336 and 111 against 179 us at
-// M=512, K=N=4096, same box.
+// M=512, K=N=4096, same box, both with the per-group float64 fold.
 struct WideLdsStage {
     // Limb li, 8-row copy block, lane slot: row r's 16-byte chunk c (k = 64 kb + 8 c .. +7)
     // at u32x4 index (r >> 1) * 16 + 8 * (r & 1) + (c ^ ((r >> 1) & 7)) of a[li].
@@ -352,12 +358,27 @@ __global__ __launch_bounds__(256) void q4_gemm_wide_kernel(const uint16_t* xs, c
     for (int tn = 0; tn < WN; ++tn) scol[tn] = ws + static_cast<size_t>(min(n0 + 16 * tn + j, N - 1)) * G;
 
     double acc[WM][WN][4];
+    float acc32[WM][WN][4];
 #pragma unroll
     for (int tm = 0; tm < WM; ++tm)
 #pragma unroll
         for (int tn = 0; tn < WN; ++tn)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[tm][tn][i] = 0.0;
+            for (int i = 0; i < 4; ++i) {
+                acc[tm][tn][i] = 0.0;
+                acc32[tm][tn][i] = 0.0f;
+            }
+    auto flush = [&]() {
+#pragma unroll
+        for (int tm = 0; tm < WM; ++tm)
+#pragma unroll
+            for (int tn = 0; tn < WN; ++tn)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    acc[tm][tn][i] += static_cast<double>(acc32[tm][tn][i]);
+                    acc32[tm][tn][i] = 0.0f;
+                }
+    };
 
     auto issue_a = [&](int kb, int st) {
 #pragma unroll
@@ -384,11 +405,11 @@ __global__ __launch_bounds__(256) void q4_gemm_wide_kernel(const uint16_t* xs, c
     auto fold = [&](const f32x4 (&P)[WM][WN], const float (&bsv)[WN]) {
 #pragma unroll
         for (int tn = 0; tn < WN; ++tn) {
-            const double sc = static_cast<double>(bsv[tn]) * kSixteenthsUnit;
+            const float sc = bsv[tn] * kSixteenthsUnit;
 #pragma unroll
             for (int tm = 0; tm < WM; ++tm)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) acc[tm][tn][i] = fma(sc, static_cast<double>(P[tm][tn][i]), acc[tm][tn][i]);
+                for (int i = 0; i < 4; ++i) acc32[tm][tn][i] = fmaf(sc, P[tm][tn][i], acc32[tm][tn][i]);
         }
     };
     auto mfma_group = [&](f32x4 (&P)[WM][WN], int st, int h) {
@@ -438,11 +459,13 @@ __global__ __launch_bounds__(256) void q4_gemm_wide_kernel(const uint16_t* xs, c
             write_b(pkn, st ^ 1);
             __syncthreads();
             if (second) fold(P, bs_cur[1]);  // P is in registers: the fold needs no LDS
+            if (((kb - kb_begin) & 3) == 3) flush();
 #pragma unroll
             for (int h = 0; h < 2; ++h)
 #pragma unroll
                 for (int tn = 0; tn < WN; ++tn) bs_cur[h][tn] = bsn[h][tn];
         }
+        flush();
     }
 
     if (lb != nullptr && blockIdx.y == 0) {
