@@ -115,7 +115,7 @@ def test_small_m_both_x_paths(session, oracle, gpu, m, n, k):
     check(oracle, got, oracle.q4gemm_packed(c.x, c.packed, c.scales, threads=threads()), label=f"small-m {m}x{n}x{k}")
 
 
-@pytest.mark.parametrize("m,n,k", [(40, 100, 32), (200, 130, 64), (129, 1, 96),
+@pytest.mark.parametrize("m,n,k", [(40, 100, 32), (200, 130, 64), (129, 1, 96), (40, 100, 14336), (64, 48, 288),
                                    (5, 1, 32), (5, 17, 96), (16, 256, 256), (17, 300, 1024), (32, 64, 64),
                                    (16, 4096, 4064), (9, 40, 128), (31, 33, 384),
                                    (33, 129, 160), (100, 300, 512), (130, 260, 1056), (256, 512, 2048)])
