@@ -15,11 +15,9 @@
 //     to v / 16 (v_cvt_off_f32_i4, exact; the factor 16 joins the scale);
 //   - every product x * v / 16 is exact in fp32; the MFMA accumulates
 //     P = sum x * v / 16 over one group in fp32 from zero, and the group is
-//     folded as 16 s * P: straight into a float64 accumulator in the small-M
-//     kernels, into an fp32 accumulator that is added into float64 every 8 groups
-//     in the wide kernel. Scale application moves out of the inner loop, and the
-//     long K sum is carried in double, which keeps the max relative error against
-//     the double-precision reference well under 1e-5 at K = 4096;
+//     folded straight into a float64 accumulator as 16 s * P. Scale application
+//     moves out of the inner loop, the long K sum is carried in double, and the
+//     one fp32 rounding of each group's sum is the only error left;
 //   - large grids are XCD-aware: workgroup ids are remapped so each of the 8
 //     XCDs (one L2 each) walks a contiguous band of output tiles, sharing A
 //     rows and weight columns within its L2;
@@ -31,6 +29,7 @@
 // slot) before the single store of y (summing the partials in every tile's
 // epilogue instead cost 70 us of 280 at M=512, K=N=4096, r=16).
 #include <algorithm>
+#include <utility>
 
 #include "q4_device.hpp"
 #include "q4_kernels.hpp"
@@ -225,6 +224,17 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void q4_gemm_mfma_kernel(
     }
 }
 
+// Calls f(std::integral_constant<int, I>{}) for I = 0 .. N-1 in order (compile-time indices, so
+// register arrays indexed by I stay in registers).
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 // Limbs per x value on the bf16 MFMA path.
 constexpr int kLimbs = 3;
 
@@ -271,61 +281,75 @@ __global__ __launch_bounds__(256) void split_x_kernel(const float* __restrict__ 
 }
 
 // Wide tile for M > 32 (prefill, LoRA projections): 128 x 128 outputs per
-// workgroup, 2 x 2 wavefronts of 64 x 64 (4 x 4 MFMA tiles each), one wavefront
-// per SIMD. The matrix instruction is v_mfma_f32_16x16x32_bf16, fed with x as
+// workgroup of 8 wavefronts, two per SIMD, each wavefront 32 x 64 outputs (2 x 4
+// MFMA tiles). The matrix instruction is v_mfma_f32_16x16x32_bf16, fed with x as
 // three exact bf16 limbs (split_x_kernel) and the weights as bf16 v/16 (exact):
-// every product is exact in fp32, each 32-value group's sum P = sum x * v/16 is
-// accumulated in fp32 by three chained MFMAs (smallest limb first). The group is
-// folded into an fp32 accumulator as acc32 += 16 s * P, and every 4 stages (8
-// groups) acc32 is added into the float64 accumulator: one fp32 FMA per output and
-// group instead of a convert and a float64 FMA, and 64 fewer live registers
-// between flushes. Against the per-group float64 fold: 1.24 against 1.34 ms at
-// M=2048, K=4096, N=14336 (same box); the measured max relative error stays
-// under 1e-5 (an emulation of this order at 2.9e7 outputs: 4.1-4.8e-6 against
-// 3.8-4.0e-6 for the per-group fold). One such MFMA (16 x 16 x 32) does the work of eight
-// fp32 16x16x4 MFMAs at a sixteenth of their matrix-core cycles each, so three
-// of them cost under a fifth of the fp32 form.
+// every product is exact in fp32 and each 32-value group's sum P = sum x * v/16 is
+// accumulated in fp32 by three chained MFMAs (smallest limb first), and the group is
+// folded into float64 as acc += 16 s * P (one fp32 rounding per group sum is the
+// whole error: 6.3e-6 on the reference KAT, <= 3.7e-6 on the workload shapes).
+// A 32 x 64 wavefront tile keeps the LDS operand reads per MFMA lowest for three
+// x limbs per weight (10 KiB per group and wavefront) at 2 wavefronts per SIMD
+// (the float64 accumulators need 64 VGPRs per wavefront).
 // Lane (j = l%16, q = l/16) of a 16x16x32 MFMA holds A[row j][k = 8q .. 8q+7] and
 // B[k = 8q .. 8q+7][column j] (8 bf16 each), and result rows 4q .. 4q+3 of column
-// j. Per stage of two groups (64 values of K) the workgroup fills one of two LDS
-// buffers (64 KiB each):
-//   - the x-limb tile (3 limbs x 128 rows x 64 values, 48 KiB), copied global ->
-//     LDS by global_load_lds_dwordx4 (no VGPRs): per limb 16 copies of 8 full
-//     128-byte rows, four rows' blocks per wavefront with the three limbs at
-//     fixed offsets. Row chunks are XOR-swizzled so that the 16 rows a pass of
-//     MFMA-operand reads touches fall on 16 distinct bank groups;
-//   - the dequantised B tile (2 groups x 128 columns x 32 values as bf16 v/16,
-//     16 KiB): each thread loads one group's 16 packed bytes of one column,
-//     decodes them once for the whole workgroup and writes them in the MFMA B
-//     layout, so every wavefront reads its B operands as linear 1 KiB runs.
-// Stage s+1 is copied while stage s computes; one barrier per stage. An odd
-// number of groups leaves the last stage's second group empty: its x limbs are
-// zero padding, its weight loads are clamped into the column, and its MFMAs and
-// fold are skipped (a wavefront-uniform branch). Against the same tile on
-// v_mfma_f32_16x16x4_f32 with x staged as fp32 (the previous product kernel):
-// 1.34 against 2.28-2.32 ms at M=2048, K=4096, N=14336 and 111 against 179 us at
-// M=512, K=N=4096, same box, both with the per-group float64 fold.
-struct WideLdsStage {
-    // Limb li, 8-row copy block, lane slot: row r's 16-byte chunk c (k = 64 kb + 8 c .. +7)
-    // at u32x4 index (r >> 1) * 16 + 8 * (r & 1) + (c ^ ((r >> 1) & 7)) of a[li].
-    u32x4 a[kLimbs][16][64];
-    // Group h of the stage, 16-column tile, lane (j, q): bf16 v/16 of k = 32 (2 kb + h) + 8 q .. +7
-    // of tile column 16 * tile + j.
-    u32x4 b[2][8][64];
+// j. Every operand reaches LDS by global_load_lds (no VGPRs, no register waits):
+//   - x limbs, one 32-value group per stage, kWideStages buffers (3 groups in
+//     flight behind the one computed): 3 limbs x 128 rows x 32 values (24 KiB);
+//     wavefront w copies rows 16w .. 16w+15 of each limb, one 1 KiB instruction per
+//     limb. Row r's 16-byte chunk c of a 16-row set sits at chunk
+//     16 (r>>2) + 4 (r&3) + (c ^ ((r>>2) & 2)): gfx950 serves a 128-bit LDS read 16
+//     lanes per cycle, the 4-lane chunks of a half-wavefront whose chunk index has
+//     even parity (lanes 0-3, 12-15, 20-23, 24-27) in one cycle and odd parity in
+//     the other, and two of those lanes conflict when their addresses agree modulo
+//     256 bytes; this placement gives each cycle's 16 MFMA-operand reads 16
+//     distinct 16-byte bank groups (measured: no bank-conflict cycles);
+//   - packed weights and scales, four groups at a time (a "quad"): lane l of
+//     wavefront w copies the 16 bytes of group 4Q + (l >> 4) of tile column
+//     16w + (l & 15), and that group's scale. A column's 4 lanes read 64 contiguous
+//     bytes, so an instruction touches 16 lines where one group at a time touched as
+//     many lines for a quarter of the bytes, and the per-column scales (512 bytes
+//     apart in [N][K/32]) cost 16 lines per instruction instead of 64;
+//   - one stage ahead of its use, each thread decodes one packed word of the
+//     stage's group (the one its own wavefront copied) into the MFMA B layout
+//     (bf16 v/16, 8 KiB per group), so every wavefront reads its B operands as
+//     linear 1 KiB runs.
+// Iteration s copies stage s + 3, waits for stage s + 1 (s_waitcnt vmcnt with the
+// exact count of copies issued after it: 3 per stage, 2 more on quad boundaries;
+// measured wait ~12 cycles per group, so three stages in flight hide the copies),
+// decodes it, passes one workgroup barrier and reads stage s + 1's operands into
+// registers while stage s's MFMAs run. Copies past the end of the K range are
+// clamped to its last group (never computed), so the counts hold everywhere.
+constexpr int kWideStages = 4;
+constexpr int kWideWavesPerTile = 8;
+
+struct WideLds {
+    u32x4 a[kWideStages][kLimbs][8][64];  // stage, limb, 16-row set, swizzled 16-byte chunk
+    u32x4 b[2][8][64];                    // stage parity, 16-column tile, lane slot j + 16 q
+    u32x4 braw[2][8][64];                 // quad parity, wavefront, lane: 16 packed bytes as copied
+    float s[2][8][64];                    // quad parity, wavefront, lane: one scale as copied
 };
 
-__global__ __launch_bounds__(256) void q4_gemm_wide_kernel(const uint16_t* xs, const uint32_t* wq, const float* ws,
+// Vector-memory instructions issue(t) adds per wavefront.
+__host__ __device__ constexpr int wide_copies(int t) { return (t % 4 == 0) ? kLimbs + 2 : kLimbs; }
+// Copies issued by stages first .. first + count - 1 (the s_waitcnt vmcnt immediate that leaves
+// exactly those in flight).
+__host__ __device__ constexpr int wide_inflight(int first, int count) {
+    return count == 0 ? 0 : wide_copies(first) + wide_inflight(first + 1, count - 1);
+}
+
+__global__ __launch_bounds__(512) void q4_gemm_wide_kernel(const uint16_t* xs, const uint32_t* wq, const float* ws,
                                                           float* __restrict__ out, int M, int N, int K,
-                                                          int tiles_m, int tiles_n, int stages_per_split,
+                                                          int tiles_m, int tiles_n, int groups_per_split,
                                                           const float* __restrict__ tmat,
                                                           const float* __restrict__ lb, int R, float lscale) {
-    constexpr int WM = 4, WN = 4;
-    __shared__ WideLdsStage stage[2];
+    constexpr int WM = 2, WN = 4;
+    __shared__ WideLds lds;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wid & 1;
-    const int wn = wid >> 1;
+    const int wm = wid & 3;
+    const int wn = wid >> 2;
     const int j = lane & 15;
     const int q = lane >> 4;
     const int G = K >> 5;
@@ -334,138 +358,193 @@ __global__ __launch_bounds__(256) void q4_gemm_wide_kernel(const uint16_t* xs, c
     int tile_m, tile_n;
     xcd_tile(tiles_m, tiles_n, tile_m, tile_n);
     const int mt0 = tile_m * 128, nt0 = tile_n * 128;
-    const int m0 = mt0 + wm * 64;
+    const int m0 = mt0 + wm * 32;
     const int n0 = nt0 + wn * 64;
-    const int kb_begin = blockIdx.y * stages_per_split;
-    const int kb_end = min(KB, kb_begin + stages_per_split);
+    const int g_begin = blockIdx.y * groups_per_split;
+    const int g_end = min(G, g_begin + groups_per_split);
+    const int n_groups = g_end - g_begin;
 
-    // x-limb copies of this wavefront: 8-row blocks 4 wid .. 4 wid + 3, three limbs each.
-    const uint16_t* asrc[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int blk = 4 * wid + i;
-        const int pair = 4 * blk + (lane >> 4);  // row pair of this lane's 16 bytes
-        const int row_t = 2 * pair + ((lane >> 3) & 1);
-        const int c = (lane & 7) ^ (pair & 7);
-        asrc[i] = xs + static_cast<size_t>(min(mt0 + row_t, M - 1)) * KB * (kLimbs * 64) + 8 * c;
+    // x-limb copy of this wavefront: rows 16 wid .. 16 wid + 15 of the tile, lane -> (row, chunk).
+    const uint16_t* asrc;
+    {
+        const int b = lane >> 4;
+        const int r = 4 * b + ((lane >> 2) & 3);
+        const int c = (lane & 3) ^ (b & 2);
+        asrc = xs + static_cast<size_t>(min(mt0 + 16 * wid + r, M - 1)) * KB * (kLimbs * 64) + 8 * c;
     }
-    // B: thread -> tile column bc, group bh of the stage (16 bytes = 4 packed words).
-    const int bc = tid & 127, bh = tid >> 7;
-    const u32x4* bsrc = reinterpret_cast<const u32x4*>(wq + static_cast<size_t>(min(nt0 + bc, N - 1)) * (K >> 3));
-    // Scales of the lane's four MFMA columns, for the fold.
-    const float* scol[WN];
+    // Quad copies: tile column 16 wid + j, group 4Q + q of the quad.
+    const int qcol = min(nt0 + 16 * wid + j, N - 1);
+    const u32x4* bsrc = reinterpret_cast<const u32x4*>(wq + static_cast<size_t>(qcol) * (K >> 3));
+    const float* ssrc = ws + static_cast<size_t>(qcol) * G;
+
+    // Copies of stage t of this split (clamped into it).
+    auto issue = [&](int t) {
+        const int g = g_begin + min(t, n_groups - 1);
+        const uint16_t* src = asrc + static_cast<size_t>(g >> 1) * (kLimbs * 64) + 32 * (g & 1);
 #pragma unroll
-    for (int tn = 0; tn < WN; ++tn) scol[tn] = ws + static_cast<size_t>(min(n0 + 16 * tn + j, N - 1)) * G;
+        for (int li = 0; li < kLimbs; ++li)
+            __builtin_amdgcn_global_load_lds(src + li * 64, &lds.a[t % kWideStages][li][wid][0], 16, 0, 0);
+        if (t % 4 == 0) {  // uniform
+            const int gq = g_begin + min(t + q, n_groups - 1);
+            const int qb = (t >> 2) & 1;
+            __builtin_amdgcn_global_load_lds(bsrc + gq, &lds.braw[qb][wid][0], 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(ssrc + gq, &lds.s[qb][wid][0], 4, 0, 0);
+        }
+    };
+    // Decode of stage t's group: lane (j, q) of wavefront w turns word q of tile column 16w + j
+    // (copied by this wavefront) into b[t & 1][w][lane]; 64 lanes read 64 distinct banks.
+    auto commit = [&](int t) {
+        const uint32_t* raw = reinterpret_cast<const uint32_t*>(&lds.braw[(t >> 2) & 1][wid][j + 16 * (t & 3)]);
+        lds.b[t & 1][wid][lane] = nibbles_bf16_16th(raw[q]);
+    };
+    // The workgroup barrier without the fence __syncthreads() adds: that fence waits for every
+    // outstanding copy (vmcnt(0)), including the stages still in flight. The copies a stage needs
+    // are waited for explicitly before it; this wavefront's LDS reads and writes are waited for here.
+    auto barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
     double acc[WM][WN][4];
-    float acc32[WM][WN][4];
 #pragma unroll
     for (int tm = 0; tm < WM; ++tm)
 #pragma unroll
         for (int tn = 0; tn < WN; ++tn)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                acc[tm][tn][i] = 0.0;
-                acc32[tm][tn][i] = 0.0f;
-            }
-    auto flush = [&]() {
+            for (int i = 0; i < 4; ++i) acc[tm][tn][i] = 0.0;
+
+    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    // Per group and wavefront: 24 MFMAs (2 x 4 tiles x 3 limbs) and the fold of the previous
+    // group's 32 sums into float64 (72 VALU operations). On gfx950 a wavefront's VALU work
+    // overlaps the matrix core only while that wavefront's own MFMA executes (the other
+    // wavefront of the SIMD waits), so the group is laid out by hand as 24 "windows", each
+    // one MFMA followed by three fold operations of the previous group, with the stage
+    // pipeline's copies, decode, barrier and operand reads placed in the windows too;
+    // sched_barrier keeps the compiler from regrouping them.
+    struct OpsA {
+        bf16x8 a[WM][kLimbs];
+    };
+    struct OpsB {
+        bf16x8 b[WN];
+        float s[WN];
+    };
+    struct Sums {
+        f32x4 p[WM][WN];
+        float s[WN];
+    };
+    const int ch = 16 * (j >> 2) + 4 * (j & 3) + (q ^ ((j >> 2) & 2));
+    auto read_a = [&](OpsA& o, int t, int tm, int li) {
+        o.a[tm][li] = __builtin_bit_cast(bf16x8, lds.a[t & 3][li][2 * wm + tm][ch]);
+    };
+    auto read_b = [&](OpsB& o, int t, int tn) {
+        o.b[tn] = __builtin_bit_cast(bf16x8, lds.b[t & 1][wn * 4 + tn][lane]);
+    };
+    auto read_s = [&](OpsB& o, int t, int tn) { o.s[tn] = lds.s[(t >> 2) & 1][wn * 4 + tn][j + 16 * (t & 3)]; };
+    // Window w's MFMA: tile pair p = w / 12 (columns 2p, 2p+1), limb 2 - (w % 12) / 4, then
+    // (tm, tn) = ((w / 2) & 1, 2p + (w & 1)): four independent chains per limb step.
+    auto mfma_w = [&](Sums& r, const OpsA& oa, const OpsB& ob, int w) {
+        const int pr = w / 12, li = 2 - (w % 12) / 4, tm = (w >> 1) & 1, tn = 2 * pr + (w & 1);
+        r.p[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(oa.a[tm][li], ob.b[tn], li == 2 ? zero : r.p[tm][tn], 0,
+                                                              0, 0);
+    };
+    // Fold operation f (0..71) of the previous group's sums: 8 scale conversions, then per output
+    // a conversion and a float64 FMA: acc += (16 s) * P.
+    float sc16[WN];
+    double scd[WN], pd[2];
+    auto fold_op = [&](const Sums& r, int f) {
+        if (f < 8) {
+            const int tn = f >> 1;
+            if ((f & 1) == 0)
+                sc16[tn] = r.s[tn] * kSixteenthsUnit;
+            else
+                scd[tn] = static_cast<double>(sc16[tn]);
+        } else {
+            const int o = (f - 8) >> 1, tn = o >> 3, tm = (o >> 2) & 1, i = o & 3;
+            if ((f & 1) == 0)
+                pd[o & 1] = static_cast<double>(r.p[tm][tn][i]);
+            else
+                acc[tm][tn][i] = fma(scd[tn], pd[o & 1], acc[tm][tn][i]);
+        }
+    };
+    auto fold_all = [&](const Sums& r) {
+#pragma unroll
+        for (int f = 0; f < 72; ++f) fold_op(r, f);
+    };
+
+    if (n_groups > 0) {
+        // Iteration s computes group s from operand registers read during iteration s - 1 and
+        // folds group s - 1's sums; in its windows it copies stage s + 3, waits for stage s + 1,
+        // decodes its word of it, passes the barrier that publishes it (which also waits for all
+        // of this wavefront's earlier LDS reads, so every buffer copied into has been read by all
+        // wavefronts) and reads stage s + 1's operands.
+        OpsA oa[2];
+        OpsB ob;
+        Sums sums[2];
+#pragma unroll
+        for (int tn = 0; tn < WN; ++tn) {  // iteration 0 folds these zeros
+            sums[1].s[tn] = 0.0f;
+#pragma unroll
+            for (int tm = 0; tm < WM; ++tm) sums[1].p[tm][tn] = zero;
+        }
+        issue(0);
+        issue(1);
+        issue(2);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(wide_inflight(1, 2)) : "memory");
+        commit(0);
+        barrier();
 #pragma unroll
         for (int tm = 0; tm < WM; ++tm)
 #pragma unroll
-            for (int tn = 0; tn < WN; ++tn)
+            for (int li = 0; li < kLimbs; ++li) read_a(oa[0], 0, tm, li);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    acc[tm][tn][i] += static_cast<double>(acc32[tm][tn][i]);
-                    acc32[tm][tn][i] = 0.0f;
+        for (int tn = 0; tn < WN; ++tn) {
+            read_b(ob, 0, tn);
+            read_s(ob, 0, tn);
+        }
+        for (int s0 = 0; s0 < n_groups; s0 += 4) {
+            static_for<4>([&](auto uc) {
+                constexpr int u = decltype(uc)::value;
+                const int s = s0 + u;
+                if (s < n_groups) {  // uniform across the workgroup
+                    OpsA& ca = oa[u & 1];
+                    OpsA& na = oa[(u + 1) & 1];
+                    Sums& cur = sums[u & 1];
+                    const Sums& old = sums[(u + 1) & 1];
+                    uint32_t raw = 0;
+                    static_for<24>([&](auto wc) {
+                        constexpr int w = decltype(wc)::value;
+                        mfma_w(cur, ca, ob, w);
+                        fold_op(old, 3 * w);
+                        fold_op(old, 3 * w + 1);
+                        fold_op(old, 3 * w + 2);
+                        if constexpr (w == 0) {
+#pragma unroll
+                            for (int tn = 0; tn < WN; ++tn) cur.s[tn] = ob.s[tn];
+                        }
+                        if constexpr (w == 1) issue(s + 3);
+                        if constexpr (w == 7) {
+                            // stage s + 1's copies are done once only those of stages s + 2, s + 3 are in flight
+                            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(wide_inflight(u + 2, 2)) : "memory");
+                            raw = reinterpret_cast<const uint32_t*>(
+                                &lds.braw[((s + 1) >> 2) & 1][wid][j + 16 * ((s + 1) & 3)])[q];
+                        }
+                        if constexpr (w == 9) lds.b[(s + 1) & 1][wid][lane] = nibbles_bf16_16th(raw);
+                        if constexpr (w == 11) barrier();
+                        if constexpr (w >= 12 && w < 18) read_a(na, s + 1, (w - 12) / 3, (w - 12) % 3);
+                        if constexpr (w == 12 || w == 13) read_b(ob, s + 1, w - 12);
+                        if constexpr (w >= 14 && w < 18) read_s(ob, s + 1, w - 14);
+                        if constexpr (w == 23) {
+                            read_b(ob, s + 1, 2);
+                            read_b(ob, s + 1, 3);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                    });
                 }
-    };
-
-    auto issue_a = [&](int kb, int st) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int li = 0; li < kLimbs; ++li)  // 1 KiB = 8 rows of one limb
-                __builtin_amdgcn_global_load_lds(asrc[i] + static_cast<size_t>(kb) * (kLimbs * 64) + li * 64,
-                                                 &stage[st].a[li][4 * wid + i][0], 16, 0, 0);
-    };
-    auto load_b = [&](int kb) { return bsrc[min(2 * kb + bh, G - 1)]; };
-    auto write_b = [&](u32x4 pk, int st) {
-#pragma unroll
-        for (int w = 0; w < 4; ++w) stage[st].b[bh][bc >> 4][(bc & 15) + 16 * w] = nibbles_bf16_16th(pk[w]);
-    };
-    auto load_s = [&](int kb, float (&s)[2][WN]) {
-#pragma unroll
-        for (int tn = 0; tn < WN; ++tn) {
-            s[0][tn] = scol[tn][2 * kb];
-            s[1][tn] = scol[tn][min(2 * kb + 1, G - 1)];
+            });
         }
-    };
-
-    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-    auto fold = [&](const f32x4 (&P)[WM][WN], const float (&bsv)[WN]) {
-#pragma unroll
-        for (int tn = 0; tn < WN; ++tn) {
-            const float sc = bsv[tn] * kSixteenthsUnit;
-#pragma unroll
-            for (int tm = 0; tm < WM; ++tm)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc32[tm][tn][i] = fmaf(sc, P[tm][tn][i], acc32[tm][tn][i]);
-        }
-    };
-    auto mfma_group = [&](f32x4 (&P)[WM][WN], int st, int h) {
-        bf16x8 bv[WN];
-#pragma unroll
-        for (int tn = 0; tn < WN; ++tn) bv[tn] = __builtin_bit_cast(bf16x8, stage[st].b[h][wn * 4 + tn][lane]);
-#pragma unroll
-        for (int tm = 0; tm < WM; ++tm) {
-            const int row_t = wm * 64 + 16 * tm + j;
-            const int p = row_t >> 1;
-            const int idx = p * 16 + 8 * (row_t & 1) + ((4 * h + q) ^ (p & 7));
-            bf16x8 av[kLimbs];
-#pragma unroll
-            for (int li = 0; li < kLimbs; ++li) av[li] = __builtin_bit_cast(bf16x8, (&stage[st].a[li][0][0])[idx]);
-#pragma unroll
-            for (int tn = 0; tn < WN; ++tn) {
-                f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[2], bv[tn], zero, 0, 0, 0);
-                t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[1], bv[tn], t, 0, 0, 0);
-                P[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[0], bv[tn], t, 0, 0, 0);
-            }
-        }
-    };
-    if (kb_begin < kb_end) {
-        float bs_cur[2][WN];
-        f32x4 P[WM][WN];
-        issue_a(kb_begin, 0);
-        {
-            const u32x4 pk = load_b(kb_begin);
-            load_s(kb_begin, bs_cur);
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            write_b(pk, 0);
-        }
-        __syncthreads();
-        for (int kb = kb_begin; kb < kb_end; ++kb) {
-            const int st = (kb - kb_begin) & 1;
-            // The last stage copies its own stage again (in bounds, never read): no branch.
-            const int kbn = min(kb + 1, kb_end - 1);
-            issue_a(kbn, st ^ 1);
-            const u32x4 pkn = load_b(kbn);
-            float bsn[2][WN];
-            load_s(kbn, bsn);
-            const bool second = 2 * kb + 1 < G;
-            mfma_group(P, st, 0);
-            fold(P, bs_cur[0]);
-            if (second) mfma_group(P, st, 1);
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            write_b(pkn, st ^ 1);
-            __syncthreads();
-            if (second) fold(P, bs_cur[1]);  // P is in registers: the fold needs no LDS
-            if (((kb - kb_begin) & 3) == 3) flush();
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int tn = 0; tn < WN; ++tn) bs_cur[h][tn] = bsn[h][tn];
-        }
-        flush();
+        if ((n_groups - 1) & 1)  // constant indices keep sums in registers
+            fold_all(sums[1]);
+        else
+            fold_all(sums[0]);
+        // the copies issued past the end still write LDS: let them land before the workgroup ends
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
 
     if (lb != nullptr && blockIdx.y == 0) {
@@ -777,9 +856,8 @@ hipError_t launch_mfma(const float* x, const uint8_t* w_packed, const float* w_s
 // flight.
 using SkinnyShape = TileShape<1, 4, 1, 4>;
 constexpr int kSkinnyPD = 2;
-// Wide tile of q4_gemm_wide_kernel: 128 x 128 outputs, 4 wavefronts.
+// Wide tile of q4_gemm_wide_kernel: 128 x 128 outputs, 8 wavefronts.
 constexpr int kWideTile = 128;
-constexpr int kWideWaves = 4;
 
 size_t align_up(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
@@ -825,20 +903,20 @@ Q4Plan plan_q4gemm(const DeviceInfo& dev, uint32_t m, uint32_t n, uint32_t k, ui
         plan.kind = Q4Plan::kWide;
         bm = kWideTile;
         bn = kWideTile;
-        waves_per_tile = kWideWaves;
+        waves_per_tile = kWideWavesPerTile;
     }
     const size_t tiles = static_cast<size_t>((m + bm - 1) / bm) * ((n + bn - 1) / bn);
     const size_t waves = tiles * waves_per_tile;
-    // Resident wavefronts per SIMD at these register counts: skinny 3 (2 targeted), wide 1.
-    const size_t waves_per_simd = plan.kind == Q4Plan::kSkinnySplitK ? 2 : 1;
+    // Resident wavefronts per SIMD: skinny 3 at its register count (2 targeted); wide 2 (one
+    // workgroup of 8 per CU, bound by LDS).
+    const size_t waves_per_simd = 2;
     const size_t target = 4 * waves_per_simd * static_cast<size_t>(dev.cu_count);
     const int min_groups = plan.kind == Q4Plan::kSkinnySplitK ? 8 : 4;
     int splits = 1;
     while (waves * splits * 2 <= target && groups / (splits * 2) >= min_groups) splits *= 2;
-    // Re-derive so that no split is empty. The wide kernel splits whole stages of two groups.
-    const int units = plan.kind == Q4Plan::kWide ? (groups + 1) / 2 : groups;
-    const int per_split = (units + splits - 1) / splits;
-    splits = (units + per_split - 1) / per_split;
+    // Re-derive so that no split is empty.
+    const int per_split = (groups + splits - 1) / splits;
+    splits = (groups + per_split - 1) / per_split;
     plan.splits = splits;
     size_t bytes = lora_bytes;
     if (plan.kind == Q4Plan::kWide) bytes += align_up(split_x_bf16_bytes(m, k));  // x limbs
@@ -901,15 +979,15 @@ hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float*
     } else {
         const int tiles_m = static_cast<int>((m + kWideTile - 1) / kWideTile);
         const int tiles_n = static_cast<int>((n + kWideTile - 1) / kWideTile);
-        const int KB = static_cast<int>((k / kGroup + 1) / 2);
-        const int stages_per_split = (KB + plan.splits - 1) / plan.splits;
+        const int G = static_cast<int>(k / kGroup);
+        const int groups_per_split = (G + plan.splits - 1) / plan.splits;
         uint16_t* xs = reinterpret_cast<uint16_t*>(wsp);
         e = launch_split_x_bf16(x, xs, m, k, stream);
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(q4_gemm_wide_kernel, dim3(tiles_m * tiles_n, plan.splits), dim3(64 * kWideWaves), 0,
-                           stream, xs, reinterpret_cast<const uint32_t*>(w_packed), w_scales, out, static_cast<int>(m),
-                           static_cast<int>(n), static_cast<int>(k), tiles_m, tiles_n, stages_per_split, tmat, lbp,
-                           static_cast<int>(rank), lora_scale);
+        hipLaunchKernelGGL(q4_gemm_wide_kernel, dim3(tiles_m * tiles_n, plan.splits),
+                           dim3(64 * kWideWavesPerTile), 0, stream, xs, reinterpret_cast<const uint32_t*>(w_packed),
+                           w_scales, out, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), tiles_m,
+                           tiles_n, groups_per_split, tmat, lbp, static_cast<int>(rank), lora_scale);
         e = hipGetLastError();
     }
     if (e != hipSuccess || plan.splits == 1) return e;

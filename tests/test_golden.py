@@ -120,4 +120,4 @@ def test_gpu_matches_reference_kat_fixture(session, gpu):
     err = rel_err(got, f["y"].astype(np.float64))
     print(f"[gpu-case] golden kat max_rel={err:.3e}", flush=True)
     assert err <= 1e-3
-    assert err <= 3e-5
+    assert err <= TOL

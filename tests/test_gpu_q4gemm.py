@@ -63,16 +63,16 @@ def test_tiny_projection_shape(session, oracle, gpu):
 
 
 def test_reference_kat_256(session, oracle, gpu):
-    """The reference's KAT (test_q4gemm.cpp:168-176, bar 1e-3 at :49). Its scales are ~1 (not
-    0.01-0.05), so outputs are ~45 and the fp32 group partials are ~30x larger than in the
-    workload configurations: fp32 MFMA accumulation (one rounding per product) gives
-    ~2e-5 here. Held to the reference's bar and to a 3e-5 regression bound."""
+    """The reference's KAT (test_q4gemm.cpp:168-176, bar 1e-3 at :49), held to the 1e-5 bar. Its
+    scales are ~1 (not 0.01-0.05), so outputs are ~45 and each group's partial sum is ~30x larger
+    than in the workload configurations: the one fp32 rounding of every group's MFMA sum is the
+    whole error (6.3e-6 measured)."""
     note("reference KAT 256^3")
     c = reference_kat_case()
     got = session.q4gemm_values(c.x, c.packed, c.scales, 256, 256, 256)
     want = oracle.q4gemm_ref(c.x, c.b, c.scales)
     check(oracle, got, want, REF_TOL, label="kat@1e-3")
-    check(oracle, got, want, 3e-5, label="kat@3e-5")
+    check(oracle, got, want, TOL, label="kat@1e-5")
 
 
 @pytest.mark.parametrize("m", [1, 2, 3, 4])
@@ -124,6 +124,32 @@ def test_mfma_shapes(session, oracle, gpu, m, n, k):
     c = make_case(m, n, k)
     got = session.q4gemm_values(c.x, c.packed, c.scales, m, n, k)
     check(oracle, got, oracle.q4gemm_packed(c.x, c.packed, c.scales, threads=threads()), label=f"mfma {m}x{n}x{k}")
+
+
+def test_wide_one_split_many_groups(session, oracle, gpu):
+    """Wide kernel with one K split (135 tiles of 128 x 128 fill the 256 CUs at two wavefronts per
+    SIMD without splitting K) and an odd group count (33): every workgroup runs the whole K loop,
+    all four stage buffers rotate through it, and the last group has no partner."""
+    m, n, k = 1152, 1920, 1056
+    note(f"wide single split {m}x{n}x{k}")
+    c = make_case(m, n, k)
+    got = session.q4gemm_values(c.x, c.packed, c.scales, m, n, k)
+    check(oracle, got, oracle.q4gemm_packed(c.x, c.packed, c.scales, threads=threads()), label="wide 1152x1920x1056")
+
+
+def test_wide_error_model_unit_scales(session, oracle, gpu):
+    """Stress outside the workload distributions: the reference KAT's value ranges (x in [-1, 1),
+    scales in [0.5, 1.5)) at 2.2 million outputs. Above 32 rows each 32-value group is summed on
+    the bf16 MFMA in fp32 (exact products, one rounding of the group's sum of magnitude ~30 here)
+    and folded in float64, so an output near zero collects about 2^-24 x 30 per group: the max
+    relative error reaches 1.6e-5 here (the workload configurations measure <= 3.7e-6 and the
+    KAT 6.3e-6). Held to 2.5e-5, the bound this path states for unit-scale inputs."""
+    m, n, k = 1152, 1920, 1056
+    note(f"wide unit scales {m}x{n}x{k}")
+    c = make_case(m, n, k, x_dist="uniform", scale_range=(0.5, 1.5))
+    got = session.q4gemm_values(c.x, c.packed, c.scales, m, n, k)
+    check(oracle, got, oracle.q4gemm_packed(c.x, c.packed, c.scales, threads=threads()), tol=2.5e-5,
+          label="wide unit scales")
 
 
 @pytest.mark.parametrize("m", [1, 3, 24])
@@ -308,10 +334,7 @@ def test_prefill_m2048_k4096_n14336(session, oracle, gpu):
     c = make_case(m, n, k)
     x_t, w_t, s_t = to_dev(c.x, torch), to_dev(c.packed, torch), to_dev(c.scales, torch)
     y = run_device(session, torch, x_t, w_t, s_t, m, n, k).cpu().numpy()
-    rows = sorted({0, 1, 15, 16, 127, 128, 1023, 1024, 2046, 2047} | set(range(600, 606)))
-    want = np.concatenate([oracle.q4gemm_packed(c.x, c.packed, c.scales, rows=(r, r + 1), threads=threads())
-                           for r in rows])
-    check(oracle, y[rows], want, label="C4 row sample")
+    check(oracle, y, oracle.q4gemm_packed(c.x, c.packed, c.scales, threads=threads()), label="C4 all rows")
     note("prefill: x*2 -> y*2 exactly")
     y2 = run_device(session, torch, x_t * 2, w_t, s_t, m, n, k).cpu().numpy()
     assert np.array_equal(y2, 2 * y)
@@ -337,10 +360,8 @@ def test_lora_m512_k4096_n4096_r16(session, oracle, gpu):
                                y_t.data_ptr(), m, n, k, rank, alpha / rank, st.cuda_stream)
     st.synchronize()
     y = y_t.cpu().numpy()
-    rows = [0, 1, 63, 64, 255, 256, 510, 511]
-    want = np.concatenate([oracle.q4gemm_lora(c.x, c.packed, c.scales, la, lb, alpha / rank, rows=(r, r + 1),
-                                              threads=threads()) for r in rows])
-    check(oracle, y[rows], want, label="C5 row sample")
+    want = oracle.q4gemm_lora(c.x, c.packed, c.scales, la, lb, alpha / rank, threads=threads())
+    check(oracle, y, want, label="C5 all rows")
     note("lora: zero adapter equals the base projection exactly")
     z_t = torch.zeros_like(la_t)
     session.q4gemm_lora_device(x_t.data_ptr(), w_t.data_ptr(), s_t.data_ptr(), z_t.data_ptr(), lb_t.data_ptr(),
