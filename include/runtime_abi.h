@@ -104,6 +104,22 @@ int spaceslug_q4gemm_lora(const float* x, const uint8_t* w_packed, const float* 
 int spaceslug_q4gemm_device(const float* d_x, const uint8_t* d_w_packed, const float* d_w_scales,
                             float* d_y, uint32_t m, uint32_t n, uint32_t k, void* stream);
 
+/* Size of the fixed device scratch of spaceslug_q4gemm_device_noalloc (64 MiB per device). */
+#define SPACESLUG_Q4_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+/* No counterpart in the reference: for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments, contract and results as spaceslug_q4gemm_device, but the call allocates and
+ * frees nothing: the scratch its kernels need (the bf16 limbs of x above 32 rows, K-split
+ * partial sums) lives in one fixed array of SPACESLUG_Q4_NOALLOC_SCRATCH_BYTES per device,
+ * held from module load until the process ends. A shape whose scratch would exceed it
+ * returns 1 without enqueueing anything (the five workload shapes fit: 2048 x 4096 x 14336
+ * needs 48 MiB). Every call on a device shares that device's array and nothing in it needs
+ * to start at zero; calls that overlap on one device (other streams, or threads) race on it,
+ * so callers order them, e.g. on one stream. */
+int spaceslug_q4gemm_device_noalloc(const float* d_x, const uint8_t* d_w_packed, const float* d_w_scales,
+                                    float* d_y, uint32_t m, uint32_t n, uint32_t k, void* stream);
+
 /* Device-pointer, stream-ordered variant of spaceslug_q4gemm_lora. Keeps
  * T = x * lora_a (m * rank floats) and any K-split partials in the same
  * library-owned device workspace as spaceslug_q4gemm_device. */

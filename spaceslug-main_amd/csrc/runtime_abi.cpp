@@ -52,12 +52,22 @@ int from_hip(const HipError& e) {
                                           hipGetErrorString(e.code) + ")");
 }
 
-// Per-device state: launch-relevant properties and the grow-only workspace of
-// the device-pointer entry points. ws_done marks the end of the last call that
-// used the workspace, on ws_stream; a call on another stream waits for it.
+// Device scratch of spaceslug_q4gemm_device_noalloc: a module global, so each device the
+// library runs on holds its own copy from module load until the process ends, and no call
+// allocates or frees it. In host code `scratch` names a host-side stand-in, never the device
+// memory: kernels receive the per-device address that hipGetSymbolAddress returns
+// (DeviceState::scratch, queried once per device when the device's state is set up).
+constexpr size_t kNoAllocScratchBytes = SPACESLUG_Q4_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+// Per-device state: launch-relevant properties, the grow-only workspace of
+// the device-pointer entry points and the address of this device's copy of
+// `scratch`. ws_done marks the end of the last call that used the workspace, on
+// ws_stream; a call on another stream waits for it.
 struct DeviceState {
     bool ready = false;
     spaceslug::DeviceInfo info{};
+    void* scratch = nullptr;
     void* workspace = nullptr;
     size_t workspace_bytes = 0;
     hipEvent_t ws_done = nullptr;
@@ -65,8 +75,10 @@ struct DeviceState {
     bool ws_used = false;
 };
 
+// Fixed table: setting up a device's state allocates nothing on the host either.
+constexpr int kMaxDevices = 64;
 std::mutex g_device_mutex;
-std::vector<DeviceState> g_devices;
+DeviceState g_devices[kMaxDevices];
 
 // Number of visible devices, queried once (the set of devices is fixed for the process).
 int device_count() {
@@ -75,7 +87,7 @@ int device_count() {
         int count = 0;
         hipError_t e = hipGetDeviceCount(&count);
         if (e != hipSuccess || count <= 0) throw HipError{e == hipSuccess ? hipErrorNoDevice : e, "no HIP device"};
-        cached = count;
+        cached = count < kMaxDevices ? count : kMaxDevices;
     }
     return cached;
 }
@@ -84,14 +96,16 @@ DeviceState& current_device() {
     const int count = device_count();
     int id = 0;
     check(hipGetDevice(&id), "hipGetDevice");
+    if (id < 0 || id >= count) throw HipError{hipErrorInvalidDevice, "device index beyond the library's table"};
     std::lock_guard<std::mutex> lock(g_device_mutex);
-    if (g_devices.size() < static_cast<size_t>(count)) g_devices.resize(count);
     DeviceState& d = g_devices[id];
     if (!d.ready) {
         hipDeviceProp_t prop;
         check(hipGetDeviceProperties(&prop, id), "hipGetDeviceProperties");
         d.info.cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 1;
         d.info.max_lds_bytes = prop.sharedMemPerBlock;
+        // this device is current: the address is its own copy of the array
+        check(hipGetSymbolAddress(&d.scratch, HIP_SYMBOL(scratch)), "hipGetSymbolAddress (scratch)");
         d.ready = true;
     }
     return d;
@@ -398,6 +412,33 @@ int spaceslug_q4gemm_device(const float* d_x, const uint8_t* d_w_packed, const f
         return fail(SPACESLUG_ERR_DEVICE, e.what());
     } catch (...) {
         return fail(SPACESLUG_ERR_DEVICE, "spaceslug_q4gemm_device: unknown exception");
+    }
+}
+
+int spaceslug_q4gemm_device_noalloc(const float* d_x, const uint8_t* d_w_packed, const float* d_w_scales,
+                                    float* d_y, uint32_t m, uint32_t n, uint32_t k, void* stream) {
+    if (const char* why = device_call_problem(d_x, d_w_packed, d_w_scales, nullptr, nullptr, d_y, m, n, k, 0))
+        return fail(SPACESLUG_ERR_INVALID, std::string("spaceslug_q4gemm_device_noalloc: ") + why);
+    try {
+        DeviceState& dev = current_device();
+        const spaceslug::Q4Plan plan = spaceslug::plan_q4gemm(dev.info, m, n, k, 0);
+        if (plan.workspace_bytes > kNoAllocScratchBytes)
+            return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_device_noalloc: this shape needs " +
+                                                   std::to_string(plan.workspace_bytes) +
+                                                   " bytes of scratch, more than the fixed " +
+                                                   std::to_string(kNoAllocScratchBytes));
+        // every byte of scratch a call reads was written earlier in that call: nothing to clear
+        check(spaceslug::launch_q4gemm(plan, dev.info, d_x, d_w_packed, d_w_scales, d_y, m, n, k, nullptr, nullptr, 0,
+                                       0.0f, plan.workspace_bytes ? dev.scratch : nullptr,
+                                       static_cast<hipStream_t>(stream)),
+              "q4gemm launch (fixed scratch)");
+        return ok();
+    } catch (const HipError& e) {
+        return from_hip(e);
+    } catch (const std::exception& e) {
+        return fail(SPACESLUG_ERR_DEVICE, e.what());
+    } catch (...) {
+        return fail(SPACESLUG_ERR_DEVICE, "spaceslug_q4gemm_device_noalloc: unknown exception");
     }
 }
 

@@ -222,6 +222,10 @@ class BackendSession:
             if hasattr(lib, "spaceslug_q4gemm_device"):
                 lib.spaceslug_q4gemm_device.argtypes = [ctypes.c_void_p] * 4 + [_u32, _u32, _u32, ctypes.c_void_p]
                 lib.spaceslug_q4gemm_device.restype = ctypes.c_int
+            if hasattr(lib, "spaceslug_q4gemm_device_noalloc"):
+                lib.spaceslug_q4gemm_device_noalloc.argtypes = [ctypes.c_void_p] * 4 + [_u32, _u32, _u32,
+                                                                                       ctypes.c_void_p]
+                lib.spaceslug_q4gemm_device_noalloc.restype = ctypes.c_int
             if hasattr(lib, "spaceslug_q4gemm_lora_device"):
                 lib.spaceslug_q4gemm_lora_device.argtypes = ([ctypes.c_void_p] * 6 + [_u32] * 4 +
                                                              [ctypes.c_float, ctypes.c_void_p])
@@ -382,6 +386,16 @@ class BackendSession:
                                            ctypes.c_void_p(d_w_scales), ctypes.c_void_p(d_y), m, n, k,
                                            ctypes.c_void_p(stream))
         self._check(code, "q4gemm_device")
+
+    def q4gemm_device_noalloc(self, d_x: int, d_w_packed: int, d_w_scales: int, d_y: int, m: int, n: int, k: int,
+                              stream: int = 0) -> None:
+        """q4gemm_device with the library's fixed per-device scratch: allocates nothing; calls that
+        overlap on one device race on that scratch."""
+        lib = self._require("spaceslug_q4gemm_device_noalloc")
+        code = lib.spaceslug_q4gemm_device_noalloc(ctypes.c_void_p(d_x), ctypes.c_void_p(d_w_packed),
+                                                   ctypes.c_void_p(d_w_scales), ctypes.c_void_p(d_y), m, n, k,
+                                                   ctypes.c_void_p(stream))
+        self._check(code, "q4gemm_device_noalloc")
 
     def q4gemm_lora_device(self, d_x: int, d_w_packed: int, d_w_scales: int, d_lora_a: int, d_lora_b: int, d_y: int,
                            m: int, n: int, k: int, rank: int, scale: float, stream: int = 0) -> None:
