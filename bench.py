@@ -9,12 +9,14 @@ captured once into a HIP graph and replayed (the way a decode loop launches a
 fixed sequence of projections); the same sweep launched call by call from the
 host is timed too and reported as "gemv_other_launch".
 value = algorithmic bytes of all timed launches / timed wall time on the GPU
-(HIP events around the timed region, on the launch stream).
+(HIP events around exactly --steps sweeps, on the launch stream); the median of
+per-sweep times over at least 15 sweeps is reported beside it.
 
 Algorithmic bytes per launch (each tensor once): packed nibbles K*N/2 + fp32
 scales 4*N*K/32 + x 4*M*K + y 4*M*N. Flops per launch: 2*M*N*K.
 
-Also reported in the same JSON line:
+Also reported in the same JSON line, each timed as the median (with min and max) of at
+least 15 HIP-event-timed iterations after warm-up:
   - "roofline": achieved GB/s of the GEMV kernel vs MI355X's 8 TB/s HBM peak;
   - "prefill": the M=2048, K=4096, N=14336 GEMM in TFLOP/s (2*M*N*K / time, the second half of the
     headline metric). Its roofline is the matrix instruction the kernel runs: above 32 rows that is
@@ -22,22 +24,27 @@ Also reported in the same JSON line:
     3 * 2*M*N*K bf16 flops, priced against the 2.5 PFLOP/s dense bf16 peak (the fp32-equivalent rate
     and the 157.3 TFLOP/s fp32 MFMA peak are given beside it); at 32 rows or fewer the kernels run
     v_mfma_f32_16x16x4_f32, priced against 157.3 TFLOP/s;
-  - "small_batch" (M=16, K=N=4096, 32 weight copies per step) and "lora"
-    (M=512, K=N=4096, rank 16) throughput;
+  - "small_batch" (M=16, K=N=4096, 32 weight copies per step) and "lora" (M=512, K=N=4096, rank 16);
+  - "reference_bench": the reference's own q4gemm benchmark configuration (bench_q4gemm.cpp: M=N=K=1024,
+    its LCG generators and seeds, 128 warm-ups, median of 15 timed calls, TFLOP/s = 2*N^3 / time);
   - "cq4": the CQ4 codebook matmul on the reference's CQ4 benchmark shapes;
   - "launch_floor": the per-launch time of a near-empty kernel replayed the same way, and the
     fraction of the HBM peak that one launch of the GEMV's bytes could reach above it;
-  - "cpu_baseline": the C CPU oracle (double-precision restatement of the
-    reference's cpu_reference) on a bounded sample of the same GEMV workload,
-    timed on this host's cores.
-Inputs are synthetic (torch RNG on the GPU: N(0,1) activations, uniform
-nibbles in [-8, 7], scales uniform in [0.01, 0.05]).
+  - "cpu_baseline": the C CPU oracle (double-precision restatement of the reference's
+    cpu_reference) timed on this host's cores on bounded samples of the same workloads, over all
+    OpenMP threads and on one thread; the headline figure is the GEMV's, and "configs" holds the
+    other workloads;
+  - "parity": per workload, max |gpu - ref| / max(1, |ref|) of the GPU output of the timed inputs
+    against the oracle output the CPU-baseline leg computes on the same inputs (the rows it timed).
+Inputs are synthetic: torch RNG on the GPU (N(0,1) activations, uniform nibbles in [-8, 7], scales
+uniform in [0.01, 0.05]); the reference-bench leg uses the reference's own generators.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -53,6 +60,7 @@ BF16_MFMA_PEAK_TFLOPS = 2500.0
 # The library runs GEMMs of more than 32 rows on the bf16 MFMA with x as three exact bf16 limbs.
 WIDE_MIN_ROWS = 33
 BF16_LIMBS = 3
+MIN_TIMED = 15
 
 
 def gemm_roofline(m: int, n: int, k: int, seconds_per_call: float) -> dict:
@@ -62,11 +70,11 @@ def gemm_roofline(m: int, n: int, k: int, seconds_per_call: float) -> dict:
     if m >= WIDE_MIN_ROWS:
         achieved = BF16_LIMBS * tf
         return {"bound": "mfma", "instruction": "v_mfma_f32_16x16x32_bf16 (x as 3 exact bf16 limbs)",
-                "achieved": achieved, "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": achieved / BF16_MFMA_PEAK_TFLOPS, "fp32_equivalent_tflops": tf,
+                "achieved": round(achieved, 2), "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / BF16_MFMA_PEAK_TFLOPS, 4), "fp32_equivalent_tflops": round(tf, 2),
                 "fp32_mfma_peak": FP32_MFMA_PEAK_TFLOPS}
-    return {"bound": "mfma", "instruction": "v_mfma_f32_16x16x4_f32", "achieved": tf,
-            "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": tf / FP32_MFMA_PEAK_TFLOPS}
+    return {"bound": "mfma", "instruction": "v_mfma_f32_16x16x4_f32", "achieved": round(tf, 2),
+            "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
 
 
 def algo_bytes(m: int, n: int, k: int, rank: int = 0) -> int:
@@ -97,7 +105,7 @@ def make_weights(torch, n: int, k: int, copies: int, gen, with_all: bool = False
 
 
 def time_region(torch, fn, steps: int, warmup: int) -> float:
-    """Runs fn() warmup times untimed, then steps times between HIP events; returns ms per step."""
+    """Runs fn() warmup times untimed, then exactly `steps` times between two HIP events; returns ms per step."""
     stream = torch.cuda.current_stream()
     for _ in range(warmup):
         fn()
@@ -110,6 +118,24 @@ def time_region(torch, fn, steps: int, warmup: int) -> float:
     stop.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(stop) / steps
+
+
+def time_each(torch, fn, iters: int, warmup: int) -> dict:
+    """Runs fn() warmup times, then times each of `iters` (>= 15) calls between its own pair of HIP events
+    on the launch stream; returns the median, min and max in ms."""
+    iters = max(MIN_TIMED, iters)
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+    for a, b in events:
+        a.record(stream)
+        fn()
+        b.record(stream)
+    torch.cuda.synchronize()
+    ms = [a.elapsed_time(b) for a, b in events]
+    return {"median": statistics.median(ms), "min": min(ms), "max": max(ms), "iters": iters}
 
 
 def bench_gemv(torch, session, steps: int, warmup: int, copies: int = 64, launch: str = "hip-graph") -> dict:
@@ -130,6 +156,8 @@ def bench_gemv(torch, session, steps: int, warmup: int, copies: int = 64, launch
 
     sweep()
     torch.cuda.synchronize()
+    check = {"x": x.cpu().numpy(), "packed": packed[0].cpu().numpy(), "scales": scales[0].cpu().numpy(),
+             "y": ys[0].cpu().numpy()}
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         sweep()
@@ -137,8 +165,11 @@ def bench_gemv(torch, session, steps: int, warmup: int, copies: int = 64, launch
     modes = {}
     for name, fn in (("stream", sweep), ("hip-graph", g.replay)):
         ms = time_region(torch, fn, steps, warmup)
+        per = time_each(torch, fn, steps, 2)
         per_launch_s = ms * 1e-3 / copies
-        modes[name] = {"ms_per_step": ms, "per_launch_us": per_launch_s * 1e6, "gbs": bytes_per / per_launch_s / 1e9}
+        modes[name] = {"ms_per_step": ms, "per_launch_us": per_launch_s * 1e6, "gbs": bytes_per / per_launch_s / 1e9,
+                       "median_step_ms": per["median"], "min_step_ms": per["min"], "max_step_ms": per["max"],
+                       "median_gbs": bytes_per * copies / (per["median"] * 1e-3) / 1e9}
     del g
 
     # The same 64 matrices read as one matrix of 64*n columns in a single launch: what the kernel
@@ -147,53 +178,116 @@ def bench_gemv(torch, session, steps: int, warmup: int, copies: int = 64, launch
         session.q4gemm_device(x.data_ptr(), packed_all.data_ptr(), scales_all.data_ptr(), y_all.data_ptr(), m,
                               copies * n, k, torch.cuda.current_stream().cuda_stream)
 
-    ms_all = time_region(torch, one_launch, max(3, steps // 5), 2)
+    t = time_each(torch, one_launch, MIN_TIMED, 2)
     bytes_all = algo_bytes(m, copies * n, k)
-    concat = {"n": copies * n, "bytes": bytes_all, "us_per_launch": round(ms_all * 1e3, 3),
-              "gbs": round(bytes_all / (ms_all * 1e-3) / 1e9, 2),
-              "frac": round(bytes_all / (ms_all * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    concat = {"n": copies * n, "bytes": bytes_all, "us_per_launch": round(t["median"] * 1e3, 3),
+              "gbs": round(bytes_all / (t["median"] * 1e-3) / 1e9, 2),
+              "frac": round(bytes_all / (t["median"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     head = modes[launch]
-    other = {name: {"us_per_launch": round(v["per_launch_us"], 3), "gbs": round(v["gbs"], 2)}
+    other = {name: {"us_per_launch": round(v["per_launch_us"], 3), "gbs": round(v["gbs"], 2),
+                    "median_gbs": round(v["median_gbs"], 2)}
              for name, v in modes.items() if name != launch}
     return {"ms_per_step": head["ms_per_step"], "per_launch_us": head["per_launch_us"], "gbs": head["gbs"],
+            "median_step_ms": head["median_step_ms"], "min_step_ms": head["min_step_ms"],
+            "max_step_ms": head["max_step_ms"], "median_gbs": head["median_gbs"],
             "bytes_per_launch": bytes_per, "copies": copies, "launch": launch, "other_launch": other,
-            "concatenated": concat, "tflops": algo_flops(m, n, k) * 1e-12 * 1e6 / head["per_launch_us"]}
+            "concatenated": concat, "tflops": algo_flops(m, n, k) * 1e-12 * 1e6 / head["per_launch_us"],
+            "check": check}
 
 
-def bench_gemm(torch, session, m: int, n: int, k: int, copies: int, steps: int, warmup: int, rank: int = 0) -> dict:
+def bench_gemm(torch, session, m: int, n: int, k: int, copies: int, iters: int, warmup: int, rank: int = 0,
+               inputs: dict | None = None) -> dict:
+    """One step = `copies` calls over distinct weight copies; each step timed on its own, median reported.
+    The GPU output of the first call (weight copy 0) is kept with its inputs for the parity check."""
     gen = torch.Generator(device="cuda").manual_seed(99)
-    packed, scales = make_weights(torch, n, k, copies, gen)
-    x = torch.randn((m, k), dtype=torch.float32, device="cuda", generator=gen)
+    if inputs is None:
+        packed, scales = make_weights(torch, n, k, copies, gen)
+        x = torch.randn((m, k), dtype=torch.float32, device="cuda", generator=gen)
+    else:
+        packed = [torch.from_numpy(inputs["packed"]).to("cuda")] * copies
+        scales = [torch.from_numpy(inputs["scales"]).to("cuda")] * copies
+        x = torch.from_numpy(inputs["x"]).to("cuda")
     y = torch.empty((m, n), dtype=torch.float32, device="cuda")
     if rank:
         la = torch.randn((k, rank), dtype=torch.float32, device="cuda", generator=gen) * 0.02
         lb = torch.randn((rank, n), dtype=torch.float32, device="cuda", generator=gen) * 0.02
+    scale = 32.0 / rank if rank else 0.0
+
+    def call(i):
+        st = torch.cuda.current_stream().cuda_stream
+        if rank:
+            session.q4gemm_lora_device(x.data_ptr(), packed[i].data_ptr(), scales[i].data_ptr(), la.data_ptr(),
+                                       lb.data_ptr(), y.data_ptr(), m, n, k, rank, scale, st)
+        else:
+            session.q4gemm_device(x.data_ptr(), packed[i].data_ptr(), scales[i].data_ptr(), y.data_ptr(), m, n, k, st)
+
+    call(0)
+    torch.cuda.synchronize()
+    check = {"x": x.cpu().numpy(), "packed": packed[0].cpu().numpy(), "scales": scales[0].cpu().numpy(),
+             "y": y.cpu().numpy()}
+    if rank:
+        check.update(la=la.cpu().numpy(), lb=lb.cpu().numpy(), lora_scale=scale)
 
     def step():
-        st = torch.cuda.current_stream().cuda_stream
         for i in range(copies):
-            if rank:
-                session.q4gemm_lora_device(x.data_ptr(), packed[i].data_ptr(), scales[i].data_ptr(), la.data_ptr(),
-                                           lb.data_ptr(), y.data_ptr(), m, n, k, rank, 32.0 / rank, st)
-            else:
-                session.q4gemm_device(x.data_ptr(), packed[i].data_ptr(), scales[i].data_ptr(), y.data_ptr(), m, n, k,
-                                      st)
+            call(i)
 
-    ms = time_region(torch, step, steps, warmup)
-    per_call = ms * 1e-3 / copies
+    t = time_each(torch, step, iters, warmup)
+    per_call = t["median"] * 1e-3 / copies
     fl = algo_flops(m, n, k, rank)
     by = algo_bytes(m, n, k, rank)
-    tf = fl / per_call / 1e12
     return {"m": m, "n": n, "k": k, "rank": rank, "copies": copies, "ms_per_call": per_call * 1e3,
-            "tflops": tf, "gbs": by / per_call / 1e9, "flops_per_call": fl, "bytes_per_call": by,
-            "roofline": gemm_roofline(m, n, k, per_call)}
+            "min_ms_per_call": t["min"] / copies, "max_ms_per_call": t["max"] / copies, "iters": t["iters"],
+            "tflops": fl / per_call / 1e12, "gbs": by / per_call / 1e9, "flops_per_call": fl, "bytes_per_call": by,
+            "roofline": gemm_roofline(m, n, k, per_call), "check": check}
 
 
-def bench_cq4(torch, session, steps: int) -> dict:
-    """The CQ4 codebook matmul on the reference's CQ4 benchmark shapes (vulkan-runtime/bench/bench_cq4gemm.cpp:
+def lcg_stream(count: int, seed: int):
+    """The reference benchmark's Numerical Recipes LCG (bench_q4gemm.cpp:91-113): states s_1 .. s_count of
+    s <- s * 1664525 + 1013904223 (mod 2^32), computed in blocks with the composed affine map."""
+    import numpy as np
+
+    a, c, mod = 1664525, 1013904223, 1 << 32
+    block = 4096
+    first = np.empty(block, dtype=np.uint64)
+    s = seed & 0xFFFFFFFF
+    for i in range(block):
+        s = (s * a + c) % mod
+        first[i] = s
+    ab, cb = 1, 0  # map of `block` steps: s -> ab*s + cb
+    for _ in range(block):
+        ab, cb = (ab * a) % mod, (cb * a + c) % mod
+    out = np.empty(((count + block - 1) // block) * block, dtype=np.uint64)
+    cur = first
+    for b in range(0, out.size, block):
+        out[b:b + block] = cur
+        cur = (cur * np.uint64(ab) + np.uint64(cb)) & np.uint64(0xFFFFFFFF)
+    return out[:count]
+
+
+def reference_bench_inputs(n: int = 1024) -> dict:
+    """bench_q4gemm.cpp:155-163 inputs: A ~ U[-1, 1) seed 0x12345678, int4 values seed 0x9abcdef0 drawn k-major
+    (b[k*N + n] = (s >> 8) % 16 - 8), scales ~ U[0.5, 1.5) seed 0x13579bdf, packed LSB-first [n][k/2]."""
+    import numpy as np
+
+    def floats(count, seed, lo, hi):
+        u = (lcg_stream(count, seed) >> np.uint64(8)).astype(np.float32) * np.float32(1.0 / 16777216.0)
+        return (np.float32(lo) + u * np.float32(hi - lo)).astype(np.float32)
+
+    x = floats(n * n, 0x12345678, -1.0, 1.0).reshape(n, n)
+    b = ((lcg_stream(n * n, 0x9ABCDEF0) >> np.uint64(8)) % np.uint64(16)).astype(np.int16) - 8
+    b = b.reshape(n, n).astype(np.int8)  # [k][n]
+    scales = floats(n * (n // 32), 0x13579BDF, 0.5, 1.5).reshape(n, n // 32)
+    nib = (b.T.astype(np.uint8) & 0xF)  # [n][k]
+    packed = (nib[:, 0::2] | (nib[:, 1::2] << 4)).astype(np.uint8)
+    return {"x": x, "packed": np.ascontiguousarray(packed), "scales": scales}
+
+
+def bench_cq4(torch, session, iters: int) -> dict:
+    """The CQ4 codebook matmul on the reference's CQ4 bench shapes (vulkan-runtime/bench/bench_cq4gemm.cpp:
     bits 4, group 128, non-interleaved, input_scale_recip; 1024^3, 1x512x512, 1024x512x512), device-resident
-    inputs, one spaceslug_cq4_matmul_device call per step. TFLOP/s = 2*M*N*K / time, as the reference counts it
-    (transform and decode not counted)."""
+    inputs, one spaceslug_cq4_matmul_device call per iteration. TFLOP/s = 2*M*N*K / time, as the reference
+    counts it (transform and decode not counted)."""
     from spaceslug_amd.backend import CQ4MatrixStruct
 
     out = {}
@@ -215,10 +309,16 @@ def bench_cq4(torch, session, steps: int) -> dict:
         def step():
             session.cq4_matmul_device(s, a.data_ptr(), m, c.data_ptr(), torch.cuda.current_stream().cuda_stream)
 
-        reps = 20 if m > 1 else 200
-        ms = time_region(torch, lambda: [step() for _ in range(reps)], max(3, steps // 10), 2) / reps
-        out[f"{m}x{n}x{k}"] = {"us_per_call": round(ms * 1e3, 3),
-                               "tflops": round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 3)}
+        step()
+        torch.cuda.synchronize()
+        check = {"m": m, "n": n, "k": k, "gs": gs, "codebook": codebook.view(torch.int16).cpu().numpy(),
+                 "norms": norms.view(torch.int16).cpu().numpy(), "recip": recip.view(torch.int16).cpu().numpy(),
+                 "packed": packed.cpu().numpy(), "a": a.view(torch.int16).cpu().numpy(),
+                 "c": c.view(torch.int16).cpu().numpy()}
+        t = time_each(torch, step, iters, 10)
+        out[f"{m}x{n}x{k}"] = {"us_per_call": round(t["median"] * 1e3, 3), "min_us": round(t["min"] * 1e3, 3),
+                               "max_us": round(t["max"] * 1e3, 3),
+                               "tflops": round(2.0 * m * n * k / (t["median"] * 1e-3) / 1e12, 3), "check": check}
     return out
 
 
@@ -236,8 +336,8 @@ def copy_reference(torch, steps: int) -> dict:
             for b in src:
                 dst.copy_(b)
 
-        ms = time_region(torch, sweep, max(3, steps // 5), 2)
-        us = ms * 1e3 / copies
+        t = time_each(torch, sweep, MIN_TIMED, 2)
+        us = t["median"] * 1e3 / copies
         out[label] = {"bytes_read": nbytes, "bytes_written": nbytes, "us_per_launch": round(us, 3),
                       "gbs_read_plus_write": round(2 * nbytes / us / 1e3, 1)}
         del src, dst
@@ -263,9 +363,9 @@ def launch_floor(torch, steps: int, bytes_per_launch: int) -> dict:
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         sweep()
-    ms = time_region(torch, g.replay, steps, 5)
+    t = time_each(torch, g.replay, max(MIN_TIMED, steps), 5)
     del g
-    us = ms * 1e3 / len(bufs)
+    us = t["median"] * 1e3 / len(bufs)
     ideal_us = bytes_per_launch / (HBM_PEAK_GBS * 1e3)
     return {"us_per_launch": round(us, 3), "kernel": "torch fill_ of 4 bytes, 64 launches replayed as one HIP graph",
             "gemv_ceiling_frac": round(ideal_us / (us + ideal_us), 4)}
@@ -281,7 +381,12 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(budget_s: float) -> dict:
+def host_threads() -> int:
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return max(1, min(threads, os.cpu_count() or 1))
+
+
+def cpu_gemv_baseline(budget_s: float) -> dict:
     """Times the C oracle (double, from the packed bytes) on whole GEMV calls of the same shape: over
     OMP_NUM_THREADS threads (parallel over columns; every output is summed in the same order as with one
     thread) for `budget_s`, then single-threaded for a quarter of that."""
@@ -290,8 +395,7 @@ def cpu_baseline(budget_s: float) -> dict:
     from oracle import oracle as o
 
     m, n, k = 1, 14336, 4096
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    threads = max(1, min(threads, os.cpu_count() or 1))
+    threads = host_threads()
     rng = np.random.default_rng(7)
     # 16 distinct weight sets (590 MB, beyond any host last-level cache), used in turn
     pool = [(rng.integers(0, 256, size=(n, k // 2), dtype=np.uint8),
@@ -320,6 +424,84 @@ def cpu_baseline(budget_s: float) -> dict:
             "cpu_model": cpu_model(), "host_cpus": os.cpu_count()}
 
 
+def cpu_gemm_baseline(check: dict, budget_s: float, single_rows: int, bar: float = 1e-5) -> tuple[dict, dict]:
+    """Times the C oracle on the workload's own inputs: over all host threads on as many whole rows as fit in
+    `budget_s` (all rows when they fit), then on one thread on `single_rows` rows; compares the GPU output of
+    those inputs with the oracle's on every row the threaded run computed, against `bar`. Returns
+    (baseline, parity)."""
+    import numpy as np
+
+    from oracle import oracle as o
+
+    x, packed, scales, y = check["x"], check["packed"], check["scales"], check["y"]
+    m, k = x.shape
+    n = packed.shape[0]
+    rank = check["la"].shape[1] if "la" in check else 0
+    threads = host_threads()
+
+    def ref(rows, nthreads):
+        if rank:
+            return o.q4gemm_lora(x, packed, scales, check["la"], check["lb"], check["lora_scale"], rows=rows,
+                                 threads=nthreads)
+        return o.q4gemm_packed(x, packed, scales, rows=rows, threads=nthreads)
+
+    # threaded: row chunks until the budget is spent or every row is done
+    chunk = max(1, min(m, 64))
+    done, elapsed, outs = 0, 0.0, []
+    while done < m and (elapsed < budget_s or done == 0):
+        r1 = min(m, done + chunk)
+        t0 = time.perf_counter()
+        outs.append(ref((done, r1), threads))
+        elapsed += time.perf_counter() - t0
+        done = r1
+    want = np.concatenate(outs)
+    rep = o.compare(y[:done], want, bar)
+    flops = algo_flops(done, n, k, rank)
+    rows1 = min(single_rows, m)
+    t0 = time.perf_counter()
+    ref((0, rows1), 1)
+    e1 = time.perf_counter() - t0
+    flops1 = algo_flops(rows1, n, k, rank)
+    base = {"value": flops / elapsed / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"rows 0..{done - 1} of {m} (M={m} K={k} N={n}{f' r={rank}' if rank else ''}), double-precision "
+                      f"C oracle over {threads} OpenMP threads, {elapsed:.2f} s",
+            "single_thread": {"value": flops1 / e1 / 1e12, "unit": "TFLOP/s", "cores": 1,
+                              "sample": f"rows 0..{rows1 - 1} on one thread, {e1:.2f} s"}}
+    parity = {"max_rel": rep["max_relative_error"], "normwise": rep["normwise_error"], "rows_checked": done,
+              "rows": m, "bar": bar, "status": rep["status"]}
+    return base, parity
+
+
+def cpu_cq4_parity(check: dict) -> dict:
+    """The CQ4 oracle (double) on the benchmark's own matrix and activations: max |Δ| / max(1, |ref|) of the
+    fp16 output, and the max error in units of the fp16 spacing at the reference (the path's bar: half a
+    spacing plus 1e-5 relative)."""
+    import numpy as np
+
+    from oracle import cq4
+
+    W = cq4.CQ4Matrix(4, check["k"], check["n"], check["gs"], check["k"] // check["gs"], 0,
+                      check["codebook"].view(np.uint16), check["norms"].view(np.uint16), check["packed"],
+                      input_scale_recip=check["recip"].view(np.uint16))
+    ref = cq4.matmul(W, check["a"].view(np.uint16), check["m"])
+    got = check["c"].view(np.float16).astype(np.float64)
+    err = np.abs(got - ref)
+    rel = float(np.max(err / np.maximum(1.0, np.abs(ref))))
+    spacing = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+    bar = 0.5 * spacing + 1e-5 * np.maximum(1.0, np.abs(ref))
+    return {"max_rel": rel, "max_err_over_bar": float(np.max(err / bar)), "status": "pass" if np.all(err <= bar)
+            else "fail", "bar": "half an fp16 spacing + 1e-5*max(1,|ref|)"}
+
+
+def gpu_gemv_parity(check: dict) -> dict:
+    from oracle import oracle as o
+
+    ref = o.q4gemm_packed(check["x"], check["packed"], check["scales"], threads=host_threads())
+    rep = o.compare(check["y"], ref, 1e-5)
+    return {"max_rel": rep["max_relative_error"], "normwise": rep["normwise_error"], "rows_checked": 1, "rows": 1,
+            "bar": 1e-5, "status": rep["status"]}
+
+
 def load_traffic() -> float | None:
     p = REPO / "profiles" / "q4_gemv_m1_k4096_n14336_traffic.json"
     if p.is_file():
@@ -328,6 +510,10 @@ def load_traffic() -> float | None:
         except Exception:
             return None
     return None
+
+
+def strip(d: dict) -> dict:
+    return {k: v for k, v in d.items() if k != "check"}
 
 
 def main() -> int:
@@ -339,7 +525,9 @@ def main() -> int:
                     help="headline GEMV timing: the 64-launch sweep replayed as one HIP graph (default) or launched "
                          "call by call on the stream (both are measured and reported)")
     ap.add_argument("--gemv-only", action="store_true", help="skip the secondary GEMM configurations")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget (0 disables)")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="CPU baseline time budget of the GEMV and prefill samples (0 disables the CPU leg and with "
+                         "it the parity figures)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run 3 plain device copies of this many MiB (a known-traffic kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -358,6 +546,7 @@ def main() -> int:
 
     session = BackendSession()
     session.capability()  # fails loudly when the HIP library is missing
+    iters = max(MIN_TIMED, args.steps)
 
     if args.copy_calibration_mib > 0:
         n = args.copy_calibration_mib * (1 << 20) // 4
@@ -372,6 +561,7 @@ def main() -> int:
     print(f"[bench] gemv sweep steps={args.steps} warmup={args.warmup} launch={args.launch}", file=sys.stderr,
           flush=True)
     gemv = bench_gemv(torch, session, args.steps, args.warmup, launch=args.launch)
+    checks = {"gemv": gemv.pop("check")}
     result = {
         "metric": METRIC,
         "value": round(gemv["gbs"], 2),
@@ -392,6 +582,9 @@ def main() -> int:
                      "frac": round(gemv["gbs"] / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
                      "bytes_per_launch": gemv["bytes_per_launch"],
                      "avg_launch_us": round(gemv["per_launch_us"], 3)},
+        "gemv_median": {"ms_per_step": round(gemv["median_step_ms"], 4), "min_ms": round(gemv["min_step_ms"], 4),
+                        "max_ms": round(gemv["max_step_ms"], 4), "gbs": round(gemv["median_gbs"], 2),
+                        "frac": round(gemv["median_gbs"] / HBM_PEAK_GBS, 4), "iters": iters},
         "gemv_other_launch": gemv["other_launch"],
         "gemv_concatenated": gemv["concatenated"],
     }
@@ -401,26 +594,63 @@ def main() -> int:
     result["copy_reference"] = copy_reference(torch, args.steps)
     result["launch_floor"] = launch_floor(torch, args.steps, result["roofline"]["bytes_per_launch"])
     if not args.gemv_only:
+        def gemm_entry(r, unit_gbs=False):
+            e = {"value": round(r["tflops"], 3), "unit": "TFLOP/s", "ms_per_call": round(r["ms_per_call"], 4),
+                 "min_ms": round(r["min_ms_per_call"], 4), "max_ms": round(r["max_ms_per_call"], 4),
+                 "iters": r["iters"], "roofline": r["roofline"]}
+            if unit_gbs:
+                e["gbs"] = round(r["gbs"], 2)
+                e["us_per_call"] = round(r["ms_per_call"] * 1e3, 3)
+            return e
+
         print("[bench] prefill 2048x4096x14336", file=sys.stderr, flush=True)
-        pre = bench_gemm(torch, session, 2048, 14336, 4096, copies=1, steps=max(3, args.steps // 10), warmup=2)
-        result["prefill"] = {"value": round(pre["tflops"], 3), "unit": "TFLOP/s",
-                             "ms_per_call": round(pre["ms_per_call"], 4), "roofline": pre["roofline"]}
+        pre = bench_gemm(torch, session, 2048, 14336, 4096, copies=1, iters=iters, warmup=3)
+        checks["prefill"] = pre.pop("check")
+        result["prefill"] = gemm_entry(pre)
         torch.cuda.empty_cache()
         print("[bench] small batch 16x4096x4096 x32 copies", file=sys.stderr, flush=True)
-        sb = bench_gemm(torch, session, 16, 4096, 4096, copies=32, steps=max(3, args.steps // 5), warmup=2)
-        result["small_batch"] = {"value": round(sb["tflops"], 3), "unit": "TFLOP/s", "gbs": round(sb["gbs"], 2),
-                                 "us_per_call": round(sb["ms_per_call"] * 1e3, 3), "roofline": sb["roofline"]}
+        sb = bench_gemm(torch, session, 16, 4096, 4096, copies=32, iters=iters, warmup=3)
+        checks["small_batch"] = sb.pop("check")
+        result["small_batch"] = gemm_entry(sb, unit_gbs=True)
         torch.cuda.empty_cache()
         print("[bench] lora 512x4096x4096 r16", file=sys.stderr, flush=True)
-        lo = bench_gemm(torch, session, 512, 4096, 4096, copies=1, steps=max(3, args.steps // 5), warmup=2, rank=16)
-        result["lora"] = {"value": round(lo["tflops"], 3), "unit": "TFLOP/s",
-                          "us_per_call": round(lo["ms_per_call"] * 1e3, 3), "roofline": lo["roofline"]}
+        lo = bench_gemm(torch, session, 512, 4096, 4096, copies=1, iters=iters, warmup=3, rank=16)
+        checks["lora"] = lo.pop("check")
+        result["lora"] = gemm_entry(lo)
+        result["lora"]["us_per_call"] = round(lo["ms_per_call"] * 1e3, 3)
+        torch.cuda.empty_cache()
+        print("[bench] reference bench configuration 1024^3", file=sys.stderr, flush=True)
+        rb = bench_gemm(torch, session, 1024, 1024, 1024, copies=1, iters=MIN_TIMED, warmup=128,
+                        inputs=reference_bench_inputs(1024))
+        checks["reference_bench"] = rb.pop("check")
+        result["reference_bench"] = gemm_entry(rb)
+        result["reference_bench"]["protocol"] = ("bench_q4gemm.cpp: M=N=K=1024, its LCG inputs, 128 warm-ups, median "
+                                                 "of 15 timed calls, TFLOP/s = 2*N^3/time")
         torch.cuda.empty_cache()
         print("[bench] cq4 codebook matmul", file=sys.stderr, flush=True)
-        result["cq4"] = bench_cq4(torch, session, args.steps)
+        cq = bench_cq4(torch, session, iters)
+        for key, v in cq.items():
+            checks[f"cq4 {key}"] = v.pop("check")
+        result["cq4"] = cq
     if args.cpu_seconds > 0:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        result["cpu_baseline"] = cpu_gemv_baseline(args.cpu_seconds)
+        parity = {"gemv": gpu_gemv_parity(checks["gemv"])}
+        configs = {}
+        # prefill's threaded budget covers all 2048 rows on 16 host threads (~13 s), so its parity is the full
+        # output. The reference bench's inputs have unit-range scales: above 32 rows the bf16-limb path's stated
+        # bound for those is 2.5e-5 (one fp32 rounding of each group's ~30x larger partial sum); the workload
+        # configurations are held to 1e-5.
+        plan = (("prefill", max(args.cpu_seconds, 30.0), 8, 1e-5), ("small_batch", 3.0, 16, 1e-5),
+                ("lora", 6.0, 8, 1e-5), ("reference_bench", 3.0, 64, 2.5e-5))
+        for name, budget, single, bar in plan:
+            if name in checks:
+                print(f"[bench] cpu baseline + parity: {name}", file=sys.stderr, flush=True)
+                configs[name], parity[name] = cpu_gemm_baseline(checks[name], budget, single, bar)
+        for key in [c for c in checks if c.startswith("cq4 ")]:
+            parity[key] = cpu_cq4_parity(checks[key])
+        result["cpu_baseline"]["configs"] = configs
+        result["parity"] = parity
     print(json.dumps(result), flush=True)
     return 0
 
