@@ -100,7 +100,10 @@ int spaceslug_q4gemm_lora(const float* x, const uint8_t* w_packed, const float* 
  * not allocate). Calls that share a device share that workspace; the library
  * orders them: a call on a stream other than the previous user's makes its
  * stream wait (on the GPU, hipStreamWaitEvent) for that user's kernels, and
- * host threads are serialised while enqueueing. */
+ * host threads are serialised while enqueueing. A call that needs that workspace
+ * returns SPACESLUG_ERR_UNSUPPORTED, enqueueing nothing, while `stream` is being
+ * captured into a graph (the graph would keep an address a later, larger call
+ * frees): capture a spaceslug_q4_chain or use spaceslug_q4gemm_device_noalloc. */
 int spaceslug_q4gemm_device(const float* d_x, const uint8_t* d_w_packed, const float* d_w_scales,
                             float* d_y, uint32_t m, uint32_t n, uint32_t k, void* stream);
 
@@ -122,7 +125,8 @@ int spaceslug_q4gemm_device_noalloc(const float* d_x, const uint8_t* d_w_packed,
 
 /* Device-pointer, stream-ordered variant of spaceslug_q4gemm_lora. Keeps
  * T = x * lora_a (m * rank floats) and any K-split partials in the same
- * library-owned device workspace as spaceslug_q4gemm_device. */
+ * library-owned device workspace as spaceslug_q4gemm_device (and so returns
+ * SPACESLUG_ERR_UNSUPPORTED under stream capture the same way). */
 int spaceslug_q4gemm_lora_device(const float* d_x, const uint8_t* d_w_packed,
                                  const float* d_w_scales, const float* d_lora_a,
                                  const float* d_lora_b, float* d_y, uint32_t m, uint32_t n,
@@ -245,7 +249,8 @@ int spaceslug_cq4_matmul(const spaceslug_cq4_matrix* w, const uint16_t* a, uint3
 /* Device-pointer, stream-ordered variant: every array of `w` (the struct itself
  * is host memory) and a, c are device pointers. The code-basis activations (M * K
  * floats) live in the library-owned device workspace of spaceslug_q4gemm_device,
- * ordered the same way across streams. */
+ * ordered the same way across streams; under stream capture the call returns
+ * SPACESLUG_ERR_UNSUPPORTED. */
 int spaceslug_cq4_matmul_device(const spaceslug_cq4_matrix* w, const uint16_t* d_a, uint32_t m, uint16_t* d_c,
                                 void* stream);
 

@@ -207,6 +207,18 @@ int run_host(const float* x, const uint8_t* w, const float* s, const uint8_t* d_
     return ok();
 }
 
+// Returns SPACESLUG_ERR_UNSUPPORTED (with a message) when `st` is being captured into a graph,
+// else 0. For the calls that use the shared, grow-only workspace.
+int refuse_capture(hipStream_t st, const char* what) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    check(hipStreamIsCapturing(st, &cs), "hipStreamIsCapturing");
+    if (cs == hipStreamCaptureStatusNone) return 0;
+    return fail(SPACESLUG_ERR_UNSUPPORTED,
+                std::string(what) + ": this call uses the library's shared workspace, which a captured graph must "
+                                    "not hold (a later, larger call may replace it); capture a "
+                                    "spaceslug_q4_chain instead, or use spaceslug_q4gemm_device_noalloc");
+}
+
 int run_device(const float* dx, const uint8_t* dw, const float* ds, const float* dla, const float* dlb,
                float* dy, uint32_t m, uint32_t n, uint32_t k, uint32_t rank, float lora_scale,
                void* stream) {
@@ -219,6 +231,9 @@ int run_device(const float* dx, const uint8_t* dw, const float* ds, const float*
               "q4gemm launch");
         return ok();
     }
+    // A graph captured from this stream would keep the shared workspace's address, which a
+    // later, larger call frees: refuse before touching it.
+    if (const int rc = refuse_capture(st, "q4gemm")) return rc;
     // Calls that use the shared workspace are ordered across streams: a call on a
     // stream other than the previous user's waits (on the GPU) for that user's end.
     std::lock_guard<std::mutex> lock(g_device_mutex);
@@ -631,6 +646,7 @@ int spaceslug_cq4_matmul_device(const spaceslug_cq4_matrix* w, const uint16_t* d
     try {
         DeviceState& dev = current_device();
         const hipStream_t st = static_cast<hipStream_t>(stream);
+        if (const int rc = refuse_capture(st, "spaceslug_cq4_matmul_device")) return rc;
         std::lock_guard<std::mutex> lock(g_device_mutex);
         void* ws = device_workspace(dev, spaceslug::cq4_workspace_bytes(v, m));
         if (!dev.ws_done) check(hipEventCreateWithFlags(&dev.ws_done, hipEventDisableTiming), "hipEventCreateWithFlags");

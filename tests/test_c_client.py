@@ -35,6 +35,34 @@ def test_client_int4_call_on_gpu(runtime_lib_path, gpu, tmp_path):
     assert "q4gemm: PASS" in r.stdout
 
 
+REFERENCE_NATIVE_CALLER = Path("/root/reference/native/runtime_abi_test.cpp")
+
+
+def test_native_header_path_builds_a_caller(runtime_lib_path, tmp_path):
+    """native/runtime_abi.h, at the path the reference's native callers include it from, declares the same
+    ABI: the example client builds against it alone and runs its CPU part."""
+    lib_dir = runtime_lib_path.parent
+    exe = tmp_path / "client_native"
+    subprocess.run(["g++", "-std=c++17", "-O2", f"-I{REPO / 'native'}", str(SRC), f"-L{lib_dir}",
+                    "-lspaceslug_runtime", f"-Wl,-rpath,{lib_dir}", "-o", str(exe)], check=True)
+    r = subprocess.run([str(exe), "--allow-no-device"], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "vector_add: PASS" in r.stdout
+
+
+@pytest.mark.skipif(not REFERENCE_NATIVE_CALLER.is_file(), reason="reference sources not mounted here")
+def test_reference_native_caller_builds_unchanged(runtime_lib_path, tmp_path):
+    """The reference's own native caller (native/runtime_abi_test.cpp, compiled where it lies, not copied)
+    builds against native/runtime_abi.h, links against libspaceslug_runtime.so and passes."""
+    lib_dir = runtime_lib_path.parent
+    exe = tmp_path / "reference_native_caller"
+    subprocess.run(["g++", "-std=c++17", "-O2", f"-I{REPO / 'native'}", str(REFERENCE_NATIVE_CALLER),
+                    f"-L{lib_dir}", "-lspaceslug_runtime", f"-Wl,-rpath,{lib_dir}", "-o", str(exe)], check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "PASS" in r.stdout
+
+
 CHAIN_SRC = REPO / "spaceslug-main_amd" / "examples" / "tiny_projection_chain.cpp"
 ROCM = Path("/opt/rocm")
 

@@ -371,6 +371,37 @@ def test_lora_m512_k4096_n4096_r16(session, oracle, gpu):
     assert torch.equal(y_t, base)
 
 
+def test_capture_of_workspace_call_is_refused(session, oracle, gpu):
+    """A call that needs the library's shared workspace (m > 32 here) returns -4 while its stream is being
+    captured, before touching the workspace, and the capture still ends cleanly; the same call outside
+    capture then succeeds."""
+    import ctypes
+
+    import torch
+
+    m, n, k = 64, 256, 256
+    note(f"capture refusal m={m} n={n} k={k}")
+    c = make_case(m, n, k)
+    x_t, w_t, s_t = to_dev(c.x, torch), to_dev(c.packed, torch), to_dev(c.scales, torch)
+    y_t = torch.zeros((m, n), dtype=torch.float32, device="cuda:0")
+    lib = session._native()
+    side = torch.cuda.Stream()
+    run_device(session, torch, x_t, w_t, s_t, m, n, k)  # device state set up outside any capture
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        y_t.add_(1.0)
+        rc = lib.spaceslug_q4gemm_device(ctypes.c_void_p(x_t.data_ptr()), ctypes.c_void_p(w_t.data_ptr()),
+                                         ctypes.c_void_p(s_t.data_ptr()), ctypes.c_void_p(y_t.data_ptr()), m, n, k,
+                                         ctypes.c_void_p(side.cuda_stream))
+    assert rc == -4
+    assert b"workspace" in lib.spaceslug_last_error()
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.all(y_t == 1.0)
+    y = run_device(session, torch, x_t, w_t, s_t, m, n, k)
+    check(oracle, y.cpu().numpy(), oracle.q4gemm_packed(c.x, c.packed, c.scales), label="after refused capture")
+
+
 def test_device_entry_on_side_stream(session, oracle, gpu):
     import torch
 
