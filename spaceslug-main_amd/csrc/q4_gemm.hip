@@ -23,11 +23,10 @@
 //     rows and weight columns within its L2;
 //   - when the grid is too small to fill 256 CUs, K is split across
 //     blockIdx.y and a second kernel sums the partials in a fixed order.
-// LoRA: lora_t_kernel computes T = x * la on the MFMA as K-split partials,
-// split_reduce_kernel sums them once into T (M x R), and the GEMM epilogue adds
-// scale * T[rows] * lb[:, cols] with the same MFMA tile layout (r in the K
-// slot) before the single store of y (summing the partials in every tile's
-// epilogue instead cost 70 us of 280 at M=512, K=N=4096, r=16).
+// LoRA: the preparation launch that splits x into limbs also computes T = x * la on
+// the MFMA as a few K-split partials (one per 1024 values of K), and the GEMM
+// epilogue sums them (lora_t_value) and adds scale * T[rows] * lb[:, cols] with the
+// same MFMA tile layout (r in the K slot) before the single store of y.
 #include <algorithm>
 #include <utility>
 
@@ -58,6 +57,14 @@ __device__ __forceinline__ void xcd_tile(int tiles_m, int tiles_n, int& tm, int&
     }
     tm = lin % tiles_m;
     tn = lin / tiles_m;
+}
+
+// T[row][r] = the sum of its t_splits partials, in double and in split order, rounded once.
+__device__ __forceinline__ float lora_t_value(const float* __restrict__ tpart, int t_splits, int M, int R, int row,
+                                              int r) {
+    double t = 0.0;
+    for (int z = 0; z < t_splits; ++z) t += static_cast<double>(tpart[(static_cast<size_t>(z) * M + row) * R + r]);
+    return static_cast<float>(t);
 }
 
 // Operands of one 32-value group for a wavefront's WM x WN tiles.
@@ -93,7 +100,8 @@ template <int WM, int WN, int WAVES_M, int WAVES_N, int PD>
 // use (to save registers), which serialises them behind the compute.
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void q4_gemm_mfma_kernel(
     const float* x, const uint32_t* wq, const float* ws, float* __restrict__ out, int M, int N, int K, int tiles_m,
-    int tiles_n, int groups_per_split, const float* __restrict__ tmat, const float* __restrict__ lb, int R,
+    int tiles_n, int groups_per_split, const float* __restrict__ tpart, int t_splits, const float* __restrict__ lb,
+    int R,
     float lscale) {
     using Shape = TileShape<WM, WN, WAVES_M, WAVES_N>;
     const int lane = threadIdx.x & 63;
@@ -198,7 +206,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void q4_gemm_mfma_kernel(
                 f32x4 P = zero;
                 for (int r0 = 0; r0 < R; r0 += 4) {
                     const int r = r0 + q;
-                    const float av = r < R ? tmat[static_cast<size_t>(row) * R + r] : 0.0f;
+                    const float av = r < R ? lora_t_value(tpart, t_splits, M, R, row, r) : 0.0f;
                     const float bv = r < R ? lb[static_cast<size_t>(r) * N + col] : 0.0f;
                     P = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, P, 0, 0, 0);
                 }
@@ -244,9 +252,9 @@ constexpr int kLimbs = 3;
 // product of a limb with a bf16 weight v/16 is exact in fp32.
 // One thread per 8 consecutive values of a row: two 16-byte loads, three
 // 16-byte stores (one per limb), coalesced along the row.
-__global__ __launch_bounds__(256) void split_x_kernel(const float* __restrict__ x, uint16_t* __restrict__ xs,
-                                                      int M, int K, int KB) {
-    const size_t idx = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+__device__ __forceinline__ void split_x_block(const float* __restrict__ x, uint16_t* __restrict__ xs, int M, int K,
+                                              int KB, int block) {
+    const size_t idx = static_cast<size_t>(block) * 256 + threadIdx.x;
     const size_t per_row = static_cast<size_t>(KB) * 8;
     if (idx >= static_cast<size_t>(M) * per_row) return;
     const int row = static_cast<int>(idx / per_row);
@@ -278,6 +286,11 @@ __global__ __launch_bounds__(256) void split_x_kernel(const float* __restrict__ 
     uint16_t* dst = xs + (static_cast<size_t>(row) * KB + kb) * (kLimbs * 64) + c * 8;
 #pragma unroll
     for (int li = 0; li < kLimbs; ++li) *reinterpret_cast<u32x4*>(dst + li * 64) = limb[li];
+}
+
+__global__ __launch_bounds__(256) void split_x_kernel(const float* __restrict__ x, uint16_t* __restrict__ xs,
+                                                      int M, int K, int KB) {
+    split_x_block(x, xs, M, K, KB, blockIdx.x);
 }
 
 // Wide tile for M > 32 (prefill, LoRA projections): 128 x 128 outputs per
@@ -341,7 +354,7 @@ __host__ __device__ constexpr int wide_inflight(int first, int count) {
 __global__ __launch_bounds__(512) void q4_gemm_wide_kernel(const uint16_t* xs, const uint32_t* wq, const float* ws,
                                                           float* __restrict__ out, int M, int N, int K,
                                                           int tiles_m, int tiles_n, int groups_per_split,
-                                                          const float* __restrict__ tmat,
+                                                          const float* __restrict__ tpart, int t_splits,
                                                           const float* __restrict__ lb, int R, float lscale) {
     constexpr int WM = 2, WN = 4;
     __shared__ WideLds lds;
@@ -548,17 +561,32 @@ __global__ __launch_bounds__(512) void q4_gemm_wide_kernel(const uint16_t* xs, c
     }
 
     if (lb != nullptr && blockIdx.y == 0) {
+        // LoRA term on the MFMA (r in the K slot). The stage buffers are free now: the tile's 128
+        // rows of T (its partials summed) and 128 columns of lb are loaded there by the whole
+        // workgroup at once, rows padded to R + 1 floats, then read as MFMA operands.
+        static_assert(sizeof(lds.a) >= sizeof(float) * (128 * (kMaxLoraRank + 1) + kMaxLoraRank * 128),
+                      "the LoRA tiles fit in the stage buffers");
+        const int RP = R + 1;
+        float* ts = reinterpret_cast<float*>(&lds.a[0][0][0][0]);  // [128][RP]
+        float* bs = ts + 128 * RP;                                  // [R][128]
+        __syncthreads();  // every wavefront is past its last LDS read and copy
+        for (int e = tid; e < 128 * R; e += 512) {
+            const int row = e / R, r = e - row * R;
+            ts[row * RP + r] = lora_t_value(tpart, t_splits, M, R, min(mt0 + row, M - 1), r);
+            bs[e] = lb[static_cast<size_t>(e >> 7) * N + min(nt0 + (e & 127), N - 1)];
+        }
+        __syncthreads();
 #pragma unroll
         for (int tm = 0; tm < WM; ++tm) {
-            const int row = min(m0 + 16 * tm + j, M - 1);
+            const int row_t = wm * 32 + 16 * tm + j;
 #pragma unroll
             for (int tn = 0; tn < WN; ++tn) {
-                const int col = min(n0 + 16 * tn + j, N - 1);
+                const int col_t = wn * 64 + 16 * tn + j;
                 f32x4 P = zero;
                 for (int r0 = 0; r0 < R; r0 += 4) {
                     const int r = r0 + q;
-                    const float av = r < R ? tmat[static_cast<size_t>(row) * R + r] : 0.0f;
-                    const float bv = r < R ? lb[static_cast<size_t>(r) * N + col] : 0.0f;
+                    const float av = r < R ? ts[row_t * RP + r] : 0.0f;
+                    const float bv = r < R ? bs[r * 128 + col_t] : 0.0f;
                     P = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, P, 0, 0, 0);
                 }
                 const double s = static_cast<double>(lscale);
@@ -583,21 +611,27 @@ __global__ __launch_bounds__(512) void q4_gemm_wide_kernel(const uint16_t* xs, c
     }
 }
 
-// LoRA pre-pass on the MFMA: tpart[s][m][r] = sum over the groups of split s of
-// x[m][k] * la[k][r] (la is K x R row-major). One wavefront per 16 x 16 tile of
-// (rows, ranks) and split; all of the split's operands are loaded before the
-// first MFMA. Grid (ceil(M/16), ceil(R/16), t_splits).
+// LoRA pre-pass on the MFMA: tpart[z][m][r] = sum over the kLoraGroupsPerBlock groups
+// of split z of x[m][k] * la[k][r] (la is K x R row-major). One workgroup of 4
+// wavefronts per 16 x 16 tile of (rows, ranks) and split; each wavefront takes
+// kLoraGroupsPerWave groups with all of its operands loaded before its first MFMA,
+// and the four sums are added through LDS in wavefront order. The GEMM epilogues
+// add the t_splits partials of T (lora_t_value), so T needs no reduction launch.
 constexpr int kLoraGroupsPerWave = 8;
+constexpr int kLoraGroupsPerBlock = 4 * kLoraGroupsPerWave;
 
-__global__ __launch_bounds__(64) void lora_t_kernel(const float* __restrict__ x, const float* __restrict__ la,
-                                                    float* __restrict__ tpart, int M, int K, int R) {
+__device__ __forceinline__ void lora_t_block(const float* __restrict__ x, const float* __restrict__ la,
+                                             float* __restrict__ tpart, int M, int K, int R, int bx, int by,
+                                             int bz) {
+    __shared__ f32x4 red[4][64];
     const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
     const int j = lane & 15;
     const int q = lane >> 4;
     const int G = K >> 5;
-    const int m0 = blockIdx.x * 16;
-    const int r0 = blockIdx.y * 16;
-    const int g_begin = blockIdx.z * kLoraGroupsPerWave;
+    const int m0 = bx * 16;
+    const int r0 = by * 16;
+    const int g_begin = bz * kLoraGroupsPerBlock + w * kLoraGroupsPerWave;
     const int row = min(m0 + j, M - 1);
     const int r = r0 + j;
     const int rc = min(r, R - 1);
@@ -617,7 +651,7 @@ __global__ __launch_bounds__(64) void lora_t_kernel(const float* __restrict__ x,
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int i = 0; i < kLoraGroupsPerWave; ++i) {
-        if (g_begin + i < G) {  // uniform
+        if (g_begin + i < G) {  // uniform per wavefront
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
                 const float av = t < 4 ? a_lo[i][t & 3] : a_hi[i][t & 3];
@@ -626,12 +660,34 @@ __global__ __launch_bounds__(64) void lora_t_kernel(const float* __restrict__ x,
             }
         }
     }
-    float* dst = tpart + static_cast<size_t>(blockIdx.z) * M * R;
+    red[w][lane] = acc;
+    __syncthreads();
+    if (w == 0) {
+        f32x4 sum = red[0][lane];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int rr = m0 + 4 * q + i;
-        if (rr < M && r < R) dst[static_cast<size_t>(rr) * R + r] = acc[i];
+        for (int v = 1; v < 4; ++v) sum += red[v][lane];
+        float* dst = tpart + static_cast<size_t>(bz) * M * R;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int rr = m0 + 4 * q + i;
+            if (rr < M && r < R) dst[static_cast<size_t>(rr) * R + r] = sum[i];
+        }
     }
+}
+
+// One launch that prepares a call's GEMM: blocks [0, split_blocks) split x into bf16
+// limbs (split_x_block; none when the GEMM reads fp32 x), the rest compute the LoRA T
+// partials (lora_t_block, grid tiles_m_t x tiles_r x t_splits). Both only read x.
+__global__ __launch_bounds__(256) void prep_kernel(const float* __restrict__ x, uint16_t* __restrict__ xs, int M,
+                                                   int K, int KB, int split_blocks, const float* __restrict__ la,
+                                                   float* __restrict__ tpart, int R, int tiles_m_t, int tiles_r) {
+    const int b = static_cast<int>(blockIdx.x);
+    if (b < split_blocks) {
+        split_x_block(x, xs, M, K, KB, b);
+        return;
+    }
+    const int t = b - split_blocks;
+    lora_t_block(x, la, tpart, M, K, R, t % tiles_m_t, (t / tiles_m_t) % tiles_r, t / (tiles_m_t * tiles_r));
 }
 
 // Small-M GEMM (M <= 32, K % 128 == 0) with no K-split partials in memory: a
@@ -715,7 +771,8 @@ template <int KW, bool kStageX>
 // x, wq and ws are not __restrict__ for the reason given at q4_gemm_mfma_kernel.
 __global__ __launch_bounds__(64 * KW) void q4_gemm_skinny_kernel(const float* x, const uint32_t* wq, const float* ws,
                                                                 float* __restrict__ y, int M, int N, int K,
-                                                                int tiles_m, const float* __restrict__ tmat,
+                                                                int tiles_m, const float* __restrict__ tpart,
+                                                                int t_splits,
                                                                 const float* __restrict__ lb, int R, float lscale) {
     // Per wavefront: its x unit (staged form), then 256 partial sums in double.
     constexpr int kRegionFloats = kStageX ? kQuadXFloats : 512;
@@ -793,6 +850,16 @@ __global__ __launch_bounds__(64 * KW) void q4_gemm_skinny_kernel(const float* x,
     constexpr int kRedStride = kRegionFloats / 2;  // doubles per wavefront region
 #pragma unroll
     for (int r = 0; r < 4; ++r) red[wk * kRedStride + (4 * q + r) * 16 + j] = acc[r];
+    // LoRA: the tile's 16 rows of T (R values each, their partials summed) and 16 columns of lb,
+    // loaded by the whole workgroup at once rather than one dependent pair per rank per output.
+    __shared__ float lora_t_s[16 * kMaxLoraRank];
+    __shared__ float lora_b_s[kMaxLoraRank * 16];
+    if (lb != nullptr) {
+        for (int e = threadIdx.x; e < 16 * R; e += 64 * KW) {
+            lora_t_s[e] = lora_t_value(tpart, t_splits, M, R, min(m0 + e / R, M - 1), e % R);
+            lora_b_s[e] = lb[static_cast<size_t>(e >> 4) * N + min(n0 + (e & 15), N - 1)];
+        }
+    }
     __syncthreads();
     for (int e = threadIdx.x; e < 256; e += 64 * KW) {
         const int rr = m0 + (e >> 4);
@@ -804,8 +871,8 @@ __global__ __launch_bounds__(64 * KW) void q4_gemm_skinny_kernel(const float* x,
         if (lb != nullptr) {
             double t = 0.0;
             for (int r = 0; r < R; ++r)
-                t = fma(static_cast<double>(tmat[static_cast<size_t>(rr) * R + r]),
-                        static_cast<double>(lb[static_cast<size_t>(r) * N + cc]), t);
+                t = fma(static_cast<double>(lora_t_s[(e >> 4) * R + r]), static_cast<double>(lora_b_s[r * 16 + (e & 15)]),
+                        t);
             s = fma(static_cast<double>(lscale), t, s);
         }
         y[static_cast<size_t>(rr) * N + cc] = static_cast<float>(s);
@@ -836,7 +903,8 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
 
 template <int WM, int WN, int WAVES_M, int WAVES_N, int PD>
 hipError_t launch_mfma(const float* x, const uint8_t* w_packed, const float* w_scales, float* out,
-                       uint32_t m, uint32_t n, uint32_t k, int splits, const float* tmat, const float* lb,
+                       uint32_t m, uint32_t n, uint32_t k, int splits, const float* tpart, int t_splits,
+                       const float* lb,
                        uint32_t rank, float lscale, hipStream_t stream) {
     using Shape = TileShape<WM, WN, WAVES_M, WAVES_N>;
     const int tiles_m = static_cast<int>((m + Shape::kBM - 1) / Shape::kBM);
@@ -847,7 +915,7 @@ hipError_t launch_mfma(const float* x, const uint8_t* w_packed, const float* w_s
                        dim3(tiles_m * tiles_n, splits), dim3(Shape::kThreads), 0, stream, x,
                        reinterpret_cast<const uint32_t*>(w_packed), w_scales, out,
                        static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), tiles_m,
-                       tiles_n, gps, tmat, lb, static_cast<int>(rank), lscale);
+                       tiles_n, gps, tpart, t_splits, lb, static_cast<int>(rank), lscale);
     return hipGetLastError();
 }
 
@@ -884,9 +952,8 @@ Q4Plan plan_q4gemm(const DeviceInfo& dev, uint32_t m, uint32_t n, uint32_t k, ui
     const int groups = static_cast<int>(k / kGroup);
     size_t lora_bytes = 0;
     if (rank > 0) {
-        plan.t_splits = (groups + kLoraGroupsPerWave - 1) / kLoraGroupsPerWave;
+        plan.t_splits = (groups + kLoraGroupsPerBlock - 1) / kLoraGroupsPerBlock;
         lora_bytes += align_up(static_cast<size_t>(plan.t_splits) * m * rank * sizeof(float));  // T partials
-        lora_bytes += align_up(static_cast<size_t>(m) * rank * sizeof(float));                  // T
     }
     if (m <= 32 && k % (4 * kGroup) == 0) {
         plan.kind = Q4Plan::kSkinny;  // K split inside the workgroup: no partials in memory
@@ -937,22 +1004,25 @@ hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float*
         partial = reinterpret_cast<float*>(wsp);
         wsp += align_up(static_cast<size_t>(plan.splits) * m * n * sizeof(float));
     }
-    float* tmat = nullptr;
+    float* tpart = nullptr;
     if (rank > 0) {
-        float* tpart = reinterpret_cast<float*>(wsp);
+        tpart = reinterpret_cast<float*>(wsp);
         wsp += align_up(static_cast<size_t>(plan.t_splits) * m * rank * sizeof(float));
-        tmat = reinterpret_cast<float*>(wsp);
-        wsp += align_up(static_cast<size_t>(m) * rank * sizeof(float));
-        hipLaunchKernelGGL(lora_t_kernel, dim3((m + 15) / 16, (rank + 15) / 16, plan.t_splits), dim3(64), 0, stream,
-                           x, la, tpart, static_cast<int>(m), static_cast<int>(k), static_cast<int>(rank));
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-        const size_t tcount = static_cast<size_t>(m) * rank;
-        const size_t tblocks = std::min((tcount + 255) / 256, static_cast<size_t>(dev.cu_count) * 8);
-        hipLaunchKernelGGL(split_reduce_kernel, dim3(static_cast<unsigned>(tblocks)), dim3(256), 0, stream, tpart,
-                           tmat, tcount, plan.t_splits);
-        e = hipGetLastError();
-        if (e != hipSuccess) return e;
+    }
+    const int kk = static_cast<int>(k), mm = static_cast<int>(m), rr = static_cast<int>(rank);
+    // One preparation launch: the bf16 limbs of x for the wide kernel and/or the LoRA T partials.
+    uint16_t* xs = plan.kind == Q4Plan::kWide ? reinterpret_cast<uint16_t*>(wsp) : nullptr;
+    {
+        const int KB = static_cast<int>((k / kGroup + 1) / 2);
+        const int split_blocks = xs ? static_cast<int>((static_cast<size_t>(m) * KB * 8 + 255) / 256) : 0;
+        const int tiles_m_t = static_cast<int>((m + 15) / 16), tiles_r = static_cast<int>((rank + 15) / 16);
+        const int lora_blocks = rank ? tiles_m_t * tiles_r * plan.t_splits : 0;
+        if (split_blocks + lora_blocks > 0) {
+            hipLaunchKernelGGL(prep_kernel, dim3(static_cast<unsigned>(split_blocks + lora_blocks)), dim3(256), 0,
+                               stream, x, xs, mm, kk, KB, split_blocks, la, tpart, rr, tiles_m_t, tiles_r);
+            const hipError_t pe = hipGetLastError();
+            if (pe != hipSuccess) return pe;
+        }
     }
     float* out = plan.splits > 1 ? partial : y;
     const float* lbp = rank ? lb : nullptr;
@@ -968,26 +1038,22 @@ hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float*
                                    : q4_gemm_skinny_kernel<kSkinnyWavesFew, false>)
                           : (stage ? q4_gemm_skinny_kernel<kSkinnyWavesMany, true>
                                    : q4_gemm_skinny_kernel<kSkinnyWavesMany, false>);
-        hipLaunchKernelGGL(kernel, dim3(tiles_m * tiles_n), dim3(64 * waves), 0, stream, x, wq, w_scales, y,
-                           static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), tiles_m, tmat, lbp,
-                           static_cast<int>(rank), lora_scale);
+        hipLaunchKernelGGL(kernel, dim3(tiles_m * tiles_n), dim3(64 * waves), 0, stream, x, wq, w_scales, y, mm,
+                           static_cast<int>(n), kk, tiles_m, tpart, plan.t_splits, lbp, rr, lora_scale);
         return hipGetLastError();
     }
     if (plan.kind == Q4Plan::kSkinnySplitK) {
-        e = launch_mfma<1, 4, 1, 4, kSkinnyPD>(x, w_packed, w_scales, out, m, n, k, plan.splits, tmat, lbp, rank,
-                                               lora_scale, stream);
+        e = launch_mfma<1, 4, 1, 4, kSkinnyPD>(x, w_packed, w_scales, out, m, n, k, plan.splits, tpart, plan.t_splits,
+                                               lbp, rank, lora_scale, stream);
     } else {
         const int tiles_m = static_cast<int>((m + kWideTile - 1) / kWideTile);
         const int tiles_n = static_cast<int>((n + kWideTile - 1) / kWideTile);
         const int G = static_cast<int>(k / kGroup);
         const int groups_per_split = (G + plan.splits - 1) / plan.splits;
-        uint16_t* xs = reinterpret_cast<uint16_t*>(wsp);
-        e = launch_split_x_bf16(x, xs, m, k, stream);
-        if (e != hipSuccess) return e;
         hipLaunchKernelGGL(q4_gemm_wide_kernel, dim3(tiles_m * tiles_n, plan.splits),
                            dim3(64 * kWideWavesPerTile), 0, stream, xs, reinterpret_cast<const uint32_t*>(w_packed),
-                           w_scales, out, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), tiles_m,
-                           tiles_n, groups_per_split, tmat, lbp, static_cast<int>(rank), lora_scale);
+                           w_scales, out, mm, static_cast<int>(n), kk, tiles_m, tiles_n, groups_per_split, tpart,
+                           plan.t_splits, lbp, rr, lora_scale);
         e = hipGetLastError();
     }
     if (e != hipSuccess || plan.splits == 1) return e;

@@ -13,6 +13,9 @@ namespace spaceslug {
 // Scale group along K (q4gemm.comp:41,121): one fp32 scale per 32 K values.
 constexpr int kGroup = 32;
 
+// Largest LoRA rank of the fused epilogues (SPACESLUG_Q4_MAX_LORA_RANK in runtime_abi.h).
+constexpr int kMaxLoraRank = 64;
+
 // The decode GEMV handles 1..kGemvMaxRows rows; taller inputs go to the MFMA kernels.
 constexpr int kGemvMaxRows = 4;
 

@@ -24,6 +24,8 @@
 #include "cq4_kernels.hpp"
 #include "q4_kernels.hpp"
 
+static_assert(spaceslug::kMaxLoraRank == SPACESLUG_Q4_MAX_LORA_RANK, "one LoRA rank limit");
+
 namespace {
 
 thread_local std::string g_last_error;
