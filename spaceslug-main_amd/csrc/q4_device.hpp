@@ -64,15 +64,21 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 // truncated the same way, and b2 = x - b0 - b1 has at most 8 significant bits. Both
 // subtractions are exact in fp32, so b0 + b1 + b2 == x whenever x's lowest significant bit is
 // at least 2^-133 (bf16's subnormal resolution): every |x| >= 2^-110, and zero. Below that
-// the limbs drop at most 2^-133 of x.
+// the limbs drop at most 2^-133 of x. A non-finite x travels in b0 alone, with zero lower
+// limbs: +-inf stays +-inf (so a product with v = 0 is NaN and with v != 0 is +-inf, as in
+// IEEE arithmetic on x itself), and a NaN stays a NaN (its quiet bit is set, so no payload
+// truncates to an infinity).
 __device__ __forceinline__ void split_bf16_limbs(float x, uint32_t (&b)[3]) {
-    const float b0 = __uint_as_float(__float_as_uint(x) & 0xFFFF0000u);
+    const uint32_t u = __float_as_uint(x);
+    const float b0 = __uint_as_float(u & 0xFFFF0000u);
     const float r1 = x - b0;
     const float b1 = __uint_as_float(__float_as_uint(r1) & 0xFFFF0000u);
     const float r2 = r1 - b1;
-    b[0] = __float_as_uint(b0) >> 16;
-    b[1] = __float_as_uint(b1) >> 16;
-    b[2] = __float_as_uint(r2) >> 16;
+    const uint32_t mag = u << 1;  // exponent and mantissa, sign dropped
+    const bool finite = mag < 0xFF000000u;
+    b[0] = (u >> 16) | (mag > 0xFF000000u ? 0x0040u : 0u);
+    b[1] = finite ? __float_as_uint(b1) >> 16 : 0u;
+    b[2] = finite ? __float_as_uint(r2) >> 16 : 0u;
 }
 
 // The 8 nibbles of w as bf16 v / 16, packed in element order (element t in the

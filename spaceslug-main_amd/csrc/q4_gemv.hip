@@ -333,6 +333,33 @@ __device__ __forceinline__ float pipe_partial(const PipeSlot<SPC>& slot, const X
     return acc;
 }
 
+// Columns col0 .. col0 + cpb - 1 of a row x holding an infinity or a NaN, in double
+// with every term x * (v * s) formed as the double reference forms it (q4gemm_ref,
+// test_q4gemm.cpp:102-119): such a row's outputs are all infinite or NaN, and IEEE
+// arithmetic gives the reference's pattern (inf * 0 is NaN, opposite infinities give
+// NaN) in any summation order. Lane l takes groups l, l + 64, ...; reached only for
+// non-finite x, so it is written for clarity, not speed.
+__device__ __forceinline__ void pipe_ieee_columns(const float* x, const uint32_t* __restrict__ wq,
+                                               const float* __restrict__ ws, float* __restrict__ y, int N, int G,
+                                               int col0, int cpb, int lane) {
+    for (int i = 0; i < cpb && col0 + i < N; ++i) {
+        const int col = col0 + i;
+        double acc = 0.0;
+        for (int g = lane; g < G; g += 64) {
+            const double s = static_cast<double>(ws[static_cast<size_t>(col) * G + g]);
+            for (int w = 0; w < 4; ++w) {
+                const uint32_t word = wq[(static_cast<size_t>(col) * G + g) * 4 + w];
+                for (int t = 0; t < 8; ++t) {
+                    const int v = static_cast<int>(word << (28 - 4 * t)) >> 28;
+                    acc += static_cast<double>(x[32 * g + 8 * w + t]) * (static_cast<double>(v) * s);
+                }
+            }
+        }
+        for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+        if (lane == 0) y[col] = static_cast<float>(acc);
+    }
+}
+
 template <int SPC, int D>
 __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float* x,  // not restrict: see issue_chunk
                                                                    const u32x4* __restrict__ wq,
@@ -424,6 +451,17 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
             xd.d[s][4 * q + 3] = t[3];
         }
         xd.c[s] = xcs[gl];
+    }
+    // The wavefront's lanes cover every group of x, so this test is the same in every
+    // wavefront of the grid (uniform): with a non-finite x the integer form has nothing to
+    // carry it, and the columns are taken by the IEEE path below instead.
+    bool nonfinite = false;
+#pragma unroll
+    for (int s = 0; s < SPC; ++s) nonfinite = nonfinite || __builtin_isnan(xd.c[s]);
+    if (__builtin_amdgcn_ballot_w64(nonfinite) != 0) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the prologue's column loads
+        pipe_ieee_columns(x, reinterpret_cast<const uint32_t*>(wq), ws, y, N, G, col0, cpb, lane);
+        return;
     }
 
     // Steady state, S columns per trip: issue column i + D into the free slot, then compute

@@ -227,6 +227,38 @@ def test_nan_in_x_gives_nan_outputs(session, oracle, gpu, m):
         check(oracle, got[1:], oracle.q4gemm_packed(x[1:], c.packed, c.scales), label="rows without nan")
 
 
+@pytest.mark.parametrize("m,k", [(1, 512), (1, 8192), (3, 512), (24, 512), (24, 544), (64, 512)])
+def test_nonfinite_x_matches_reference_pattern(session, oracle, gpu, m, k):
+    """Infinities and NaNs in x on every path: the integer GEMV (1 x 512), the float GEMV
+    (1 x 8192, 3 rows), the in-workgroup K split (24 x 512), the K-split kernel (24 x 544) and
+    the wide bf16-limb kernel (64 rows). Every output of a row holding a non-finite value is
+    non-finite, NaN exactly where the double reference has NaN (inf * 0, opposite infinities,
+    a NaN) and the same signed infinity elsewhere; rows without one meet the usual bar."""
+    note(f"non-finite x m={m} k={k}")
+    n = 300
+    c = make_case(m, n, k)
+    x = c.x.copy()
+    x[0, 77] = np.inf
+    if m > 1:
+        x[1, 5] = np.nan
+    if m > 2:
+        x[2, 40] = -np.inf
+        x[2, 300] = np.inf
+    if m > 3:
+        x[m - 1, k - 1] = -np.inf
+    got = session.q4gemm_values(x, c.packed, c.scales, m, n, k)
+    want = oracle.q4gemm_packed(x, c.packed, c.scales, threads=threads())
+    bad = ~np.all(np.isfinite(x), axis=1)
+    g, w = got[bad], want[bad]
+    assert np.isnan(w).any() and np.isinf(w).any()  # the case exercises both outcomes
+    assert not np.isfinite(g).any()
+    np.testing.assert_array_equal(np.isnan(g), np.isnan(w))
+    inf = np.isinf(w)
+    np.testing.assert_array_equal(g[inf], w[inf])
+    if (~bad).any():
+        check(oracle, got[~bad], want[~bad], label="finite rows")
+
+
 def test_unit_vectors_select_dequantized_rows(session, oracle, gpu):
     note("unit vectors")
     n, k = 40, 128

@@ -247,3 +247,29 @@ def test_compare_metric(oracle):
     nan = np.array([0.5, np.nan, -3.0, 0.0], dtype=np.float32)
     rep = oracle.compare(nan, exp, 1e-3)
     assert rep["status"] == "fail" and rep["first_bad_index"] == 1
+
+
+def test_reference_nonfinite_x_follows_ieee(oracle):
+    """An infinite x term is x * (v * s) as q4gemm_ref forms it (test_q4gemm.cpp:102-119):
+    NaN against a zero nibble, +-inf with the sign of x * v otherwise; opposite infinities in
+    one row give NaN, and a NaN anywhere in the row gives NaN. Hand-derived for K = 64."""
+    K, N = 64, 4
+    b = np.zeros((K, N), dtype=np.int8)
+    b[0] = [0, 3, -2, 5]     # x[0] = +inf meets these nibbles
+    b[40] = [1, 1, 2, -1]    # x[40] = -inf in row 1 (second group) meets these
+    b[7] = [7, -8, 1, 1]     # a finite term everywhere
+    scales = np.full((N, K // 32), 0.5, dtype=np.float32)
+    x = np.zeros((3, K), dtype=np.float32)
+    x[0, 0] = np.inf
+    x[0, 7] = 2.0
+    x[1, 0] = np.inf
+    x[1, 40] = -np.inf
+    x[2, 7] = np.nan
+    got = oracle.q4gemm_packed(x, oracle.pack_q4(b), scales)
+    nan, inf = np.nan, np.inf
+    want = np.array([[nan, inf, -inf, inf],      # column 0: inf * 0
+                     [nan, nan, -inf, inf],      # col 1: +inf*3, -inf*1; col 2: +inf*-2, -inf*2
+                     [nan, nan, nan, nan]])
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
+    fin = ~np.isnan(want)
+    np.testing.assert_array_equal(got[fin], want[fin])
