@@ -28,8 +28,10 @@ least 15 HIP-event-timed iterations after warm-up:
   - "reference_bench": the reference's own q4gemm benchmark configuration (bench_q4gemm.cpp: M=N=K=1024,
     its LCG generators and seeds, 128 warm-ups, median of 15 timed calls, TFLOP/s = 2*N^3 / time);
   - "cq4": the CQ4 codebook matmul on the reference's CQ4 benchmark shapes;
-  - "launch_floor": the per-launch time of a near-empty kernel replayed the same way, and the
-    fraction of the HBM peak that one launch of the GEMV's bytes could reach above it;
+  - "gemv_ceiling": the GEMV's per-launch ceiling on this runtime from measured pieces: the launch
+    floor of its own grid (an empty kernel, and one that loads 16 bytes per lane), replayed the same
+    way, plus its bytes at the best HBM read rate a streaming kernel reaches; "gemv_of_ceiling" is
+    the ceiling's time over the GEMV's;
   - "cpu_baseline": the C CPU oracle (double-precision restatement of the reference's
     cpu_reference) timed on this host's cores on bounded samples of the same workloads, over all
     OpenMP threads and on one thread; the headline figure is the GEMV's, and "configs" holds the
@@ -346,29 +348,90 @@ def copy_reference(torch, steps: int) -> dict:
     return out
 
 
-def launch_floor(torch, steps: int, bytes_per_launch: int) -> dict:
-    """Per-launch time of a kernel with almost no work (torch fill_ of one float), 64 launches captured
-    into one HIP graph and replayed like the GEMV sweep: the fixed cost every launch of the sweep pays
-    (completion, cache maintenance between dependent kernels, dispatch). With it, the highest fraction of
-    the HBM peak a single launch of `bytes_per_launch` bytes could reach is
-    bytes / (floor + bytes / peak) / peak."""
-    bufs = [torch.empty(1, dtype=torch.float32, device="cuda") for _ in range(64)]
-
-    def sweep():
-        for b in bufs:
-            b.fill_(1.0)
-
-    sweep()
+def _graph_per_launch_us(torch, launch, count: int, iters: int) -> float:
+    """Median per-launch time of `count` launches captured into one HIP graph and replayed."""
+    launch_all = lambda: [launch(i) for i in range(count)]  # noqa: E731
+    launch_all()
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        sweep()
-    t = time_each(torch, g.replay, max(MIN_TIMED, steps), 5)
+        launch_all()
+    t = time_each(torch, g.replay, iters, 5)
     del g
-    us = t["median"] * 1e3 / len(bufs)
+    return t["median"] * 1e3 / count
+
+
+def gemv_grid_blocks(n: int, cu_count: int) -> tuple[int, int]:
+    """Workgroups of the single-row GEMV launch (launch_gemv_pipelined): columns per wavefront
+    4 + 5 * reps, the fewest that fit all 4-wavefront workgroups on the CUs at once."""
+    reps = 0
+    while reps < 12 and -(-n // (4 + 5 * reps)) > cu_count * 4:
+        reps += 1
+    waves = -(-n // (4 + 5 * reps))
+    return -(-waves // 4), 4 + 5 * reps
+
+
+def gemv_ceiling(torch, steps: int, m: int, n: int, k: int, bytes_per_launch: int) -> dict:
+    """The per-launch ceiling of the decode GEMV on this runtime, from three measured pieces
+    (libspaceslug_probes.so, bench-only kernels):
+      - launch floor: a kernel with no work on the GEMV's own grid, 64 launches replayed as one HIP
+        graph like the sweep (and, for comparison, torch's fill_ of 4 bytes the same way);
+      - touch floor: the same grid, one 16-byte load per lane from a column run of the GEMV's layout
+        (each of the 64 launches in its own 36.7 MB region) and one store per wavefront: a launch
+        that reaches HBM once;
+      - HBM read rate: the best of a few launch shapes of a persistent streaming read of 2.35 GB.
+    ceiling = touch floor + bytes / read rate per launch."""
+    import ctypes
+
+    import build_native
+
+    lib = ctypes.CDLL(str(build_native.probes_library_path()))
+    vp = ctypes.c_void_p
+    for fn, args in ((lib.spaceslug_probe_empty, [vp, ctypes.c_int, vp]),
+                     (lib.spaceslug_probe_touch, [vp, ctypes.c_size_t, vp, ctypes.c_int, ctypes.c_size_t, vp]),
+                     (lib.spaceslug_probe_read, [vp, ctypes.c_size_t, vp, ctypes.c_int, ctypes.c_int, vp])):
+        fn.argtypes, fn.restype = args, ctypes.c_int
+    cu = torch.cuda.get_device_properties(0).multi_processor_count
+    blocks, cpb = gemv_grid_blocks(n, cu)
+    iters = max(MIN_TIMED, steps)
+    region = 36_700_160  # one launch's weight bytes, rounded to 16
+    total = 64 * region
+    buf = torch.empty(total // 4, dtype=torch.int32, device="cuda")
+    buf.fill_(3)
+    ybuf = torch.empty(2048 * 256, dtype=torch.int32, device="cuda")
+    stream = lambda: vp(torch.cuda.current_stream().cuda_stream)  # noqa: E731
+
+    def check(rc):
+        if rc != 0:
+            raise RuntimeError(f"probe launch failed: hipError {rc}")
+
+    stride16 = cpb * (k // 2) // 16  # a wavefront's column run in the packed layout, 16-byte units
+    empty_us = _graph_per_launch_us(
+        torch, lambda i: check(lib.spaceslug_probe_empty(vp(ybuf.data_ptr()), blocks, stream())), 64, iters)
+    touch_us = _graph_per_launch_us(
+        torch, lambda i: check(lib.spaceslug_probe_touch(vp(buf.data_ptr() + i * region), region,
+                                                         vp(ybuf.data_ptr()), blocks, stride16, stream())), 64, iters)
+    fills = [torch.empty(1, dtype=torch.float32, device="cuda") for _ in range(64)]
+    fill_us = _graph_per_launch_us(torch, lambda i: fills[i].fill_(1.0), 64, iters)
+    reads = {}
+    for rb, unroll in ((512, 4), (512, 8), (1024, 4), (1024, 8), (2048, 8)):
+        t = time_each(torch, lambda: check(lib.spaceslug_probe_read(vp(buf.data_ptr()), total, vp(ybuf.data_ptr()),
+                                                                     rb, unroll, stream())), MIN_TIMED, 2)
+        reads[f"{rb}x256 threads, {unroll} loads in flight"] = round(total / (t["median"] * 1e-3) / 1e9, 1)
+    best_cfg = max(reads, key=reads.get)
+    read_gbs = reads[best_cfg]
+    del buf, ybuf, fills
+    torch.cuda.empty_cache()
+    ceiling_us = touch_us + bytes_per_launch / (read_gbs * 1e3)
     ideal_us = bytes_per_launch / (HBM_PEAK_GBS * 1e3)
-    return {"us_per_launch": round(us, 3), "kernel": "torch fill_ of 4 bytes, 64 launches replayed as one HIP graph",
-            "gemv_ceiling_frac": round(ideal_us / (us + ideal_us), 4)}
+    return {"grid": f"{blocks} workgroups x 256 threads ({cpb} columns per wavefront)",
+            "empty_us_per_launch": round(empty_us, 3), "touch_us_per_launch": round(touch_us, 3),
+            "torch_fill_us_per_launch": round(fill_us, 3),
+            "hbm_read_gbs": read_gbs, "hbm_read_best": best_cfg, "hbm_read_shapes": reads,
+            "ceiling_us_per_launch": round(ceiling_us, 3),
+            "ceiling_gbs": round(bytes_per_launch / (ceiling_us * 1e3), 1),
+            "ceiling_frac": round(ideal_us / ceiling_us, 4),
+            "peak_bound_frac": round(ideal_us / (touch_us + ideal_us), 4)}
 
 
 def cpu_model() -> str:
@@ -592,7 +655,10 @@ def main() -> int:
     torch.cuda.empty_cache()
     print("[bench] copy reference", file=sys.stderr, flush=True)
     result["copy_reference"] = copy_reference(torch, args.steps)
-    result["launch_floor"] = launch_floor(torch, args.steps, result["roofline"]["bytes_per_launch"])
+    print("[bench] gemv ceiling probes", file=sys.stderr, flush=True)
+    ceil = gemv_ceiling(torch, args.steps, 1, 14336, 4096, result["roofline"]["bytes_per_launch"])
+    ceil["gemv_of_ceiling"] = round(ceil["ceiling_us_per_launch"] / result["roofline"]["avg_launch_us"], 4)
+    result["gemv_ceiling"] = ceil
     if not args.gemv_only:
         def gemm_entry(r, unit_gbs=False):
             e = {"value": round(r["tflops"], 3), "unit": "TFLOP/s", "ms_per_call": round(r["ms_per_call"], 4),

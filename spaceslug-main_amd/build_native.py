@@ -20,6 +20,9 @@ INCLUDE = REPO_ROOT / "include"
 LIB_DIR = PACKAGE_DIR / "_lib"
 OBJ_DIR = LIB_DIR / "obj"
 LIB_NAME = "libspaceslug_runtime.so"
+# Launch-floor and HBM-read probes for the benchmark, in a library of their own.
+PROBES_SOURCE = "bench_probes.hip"
+PROBES_LIB_NAME = "libspaceslug_probes.so"
 ARCH = "gfx950"
 
 SOURCES = ["q4_gemv.hip", "q4_gemm.hip", "q4_quantize.hip", "cq4.hip", "sgemm.hip", "runtime_abi.cpp"]
@@ -54,6 +57,10 @@ def hipcc() -> str:
 
 def library_path() -> Path:
     return LIB_DIR / LIB_NAME
+
+
+def probes_library_path() -> Path:
+    return LIB_DIR / PROBES_LIB_NAME
 
 
 def _run(cmd: list[str], verbose: bool) -> None:
@@ -109,6 +116,10 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     tmp = out.with_suffix(".so.tmp")
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *[str(o) for o in objs], "-o", str(tmp)], verbose)
     os.replace(tmp, out)
+    probes = probes_library_path()
+    ptmp = probes.with_suffix(".so.tmp")
+    _run([cc, *COMMON_FLAGS, "-shared", str(CSRC / PROBES_SOURCE), "-o", str(ptmp)], verbose)
+    os.replace(ptmp, probes)
     return out
 
 
