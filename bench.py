@@ -122,22 +122,55 @@ def time_region(torch, fn, steps: int, warmup: int) -> float:
     return start.elapsed_time(stop) / steps
 
 
+_GATE = {}
+
+
+def _gate(torch, busy_us: float) -> None:
+    """Keeps the launch stream's GPU busy for about `busy_us` with device copies (256 MiB each way), so
+    that work enqueued right after it is all submitted before the GPU reaches it."""
+    if "src" not in _GATE:
+        _GATE["src"] = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+        _GATE["dst"] = torch.empty_like(_GATE["src"])
+        _GATE["dst"].copy_(_GATE["src"])
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(5):
+            _GATE["dst"].copy_(_GATE["src"])
+        torch.cuda.synchronize()
+        _GATE["copy_us"] = (time.perf_counter() - t0) * 1e6 / 5
+    for _ in range(max(1, int(busy_us / _GATE["copy_us"]) + 1)):
+        _GATE["dst"].copy_(_GATE["src"])
+
+
 def time_each(torch, fn, iters: int, warmup: int) -> dict:
     """Runs fn() warmup times, then times each of `iters` (>= 15) calls between its own pair of HIP events
-    on the launch stream; returns the median, min and max in ms."""
+    on the launch stream; returns the median, min and max in ms, and the host's submission time per call.
+    The timed calls are enqueued behind a GPU-side gate (device copies lasting about twice the host's
+    submission time of the whole loop), so the events bracket GPU execution only, as the reference's
+    timestamp queries around pre-recorded dispatches do (bench_common.cpp:25-103), and not the host's
+    Python and driver time per call."""
     iters = max(MIN_TIMED, iters)
     stream = torch.cuda.current_stream()
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
     events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+    t0 = time.perf_counter()
+    for a, b in events[:3]:
+        a.record(stream)
+        fn()
+        b.record(stream)
+    host_us = (time.perf_counter() - t0) * 1e6 / 3
+    torch.cuda.synchronize()
+    _gate(torch, 2.0 * host_us * iters + 200.0)
     for a, b in events:
         a.record(stream)
         fn()
         b.record(stream)
     torch.cuda.synchronize()
     ms = [a.elapsed_time(b) for a, b in events]
-    return {"median": statistics.median(ms), "min": min(ms), "max": max(ms), "iters": iters}
+    return {"median": statistics.median(ms), "min": min(ms), "max": max(ms), "iters": iters,
+            "host_us_per_call": host_us}
 
 
 def bench_gemv(torch, session, steps: int, warmup: int, copies: int = 64, launch: str = "hip-graph") -> dict:
@@ -241,6 +274,7 @@ def bench_gemm(torch, session, m: int, n: int, k: int, copies: int, iters: int, 
     return {"m": m, "n": n, "k": k, "rank": rank, "copies": copies, "ms_per_call": per_call * 1e3,
             "min_ms_per_call": t["min"] / copies, "max_ms_per_call": t["max"] / copies, "iters": t["iters"],
             "tflops": fl / per_call / 1e12, "gbs": by / per_call / 1e9, "flops_per_call": fl, "bytes_per_call": by,
+            "host_us_per_call": t["host_us_per_call"] / copies,
             "roofline": gemm_roofline(m, n, k, per_call), "check": check}
 
 
@@ -319,7 +353,7 @@ def bench_cq4(torch, session, iters: int) -> dict:
                  "c": c.view(torch.int16).cpu().numpy()}
         t = time_each(torch, step, iters, 10)
         out[f"{m}x{n}x{k}"] = {"us_per_call": round(t["median"] * 1e3, 3), "min_us": round(t["min"] * 1e3, 3),
-                               "max_us": round(t["max"] * 1e3, 3),
+                               "max_us": round(t["max"] * 1e3, 3), "host_us_per_call": round(t["host_us_per_call"], 2),
                                "tflops": round(2.0 * m * n * k / (t["median"] * 1e-3) / 1e12, 3), "check": check}
     return out
 
@@ -663,7 +697,7 @@ def main() -> int:
         def gemm_entry(r, unit_gbs=False):
             e = {"value": round(r["tflops"], 3), "unit": "TFLOP/s", "ms_per_call": round(r["ms_per_call"], 4),
                  "min_ms": round(r["min_ms_per_call"], 4), "max_ms": round(r["max_ms_per_call"], 4),
-                 "iters": r["iters"], "roofline": r["roofline"]}
+                 "iters": r["iters"], "host_us_per_call": round(r["host_us_per_call"], 2), "roofline": r["roofline"]}
             if unit_gbs:
                 e["gbs"] = round(r["gbs"], 2)
                 e["us_per_call"] = round(r["ms_per_call"] * 1e3, 3)

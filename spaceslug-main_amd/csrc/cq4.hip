@@ -16,12 +16,24 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <utility>
 
 #include "cq4_kernels.hpp"
 #include "q4_device.hpp"
 
 namespace spaceslug {
 namespace {
+
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+
+// f(integral_constant<int, i>) for i = 0 .. N-1, unrolled at compile time.
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 __device__ __forceinline__ float half_bits_to_float(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
 
@@ -508,6 +520,197 @@ __global__ __launch_bounds__(256) void cq4_gemm_mfma_kernel(Cq4View w, const uin
         }
 }
 
+// The same 64 x 64 tiles, operand layouts, MFMA chains and float64 fold as
+// cq4_gemm_mfma_kernel, with a deeper copy pipeline and twice the wavefronts; taken when
+// the tile's norms fit in LDS (ng <= 128, i.e. K <= 4096 at group size 32). The kernel
+// above runs one wavefront per SIMD with one 64-value stage in flight, so every LDS read,
+// copy and MFMA dependency is exposed (1024^3: ~1.7 us per stage against ~0.3 us of
+// matrix-core work). Here:
+//   - 8 wavefronts, two per SIMD: wavefront w owns rows 16 (w % 4) .. +15 and columns
+//     32 (w / 4) .. +31 of the tile (1 x 2 MFMA tiles), so one wavefront's LDS waits and
+//     VALU work (decode, fold) run while the other's MFMAs issue;
+//   - every operand reaches LDS by global_load_lds, kCq4Stages stages deep: the
+//     activation limbs (wavefront w copies the 8-row block w of each limb, three 1 KiB
+//     copies) and the packed indices as copied (4 bytes per thread: the word this thread
+//     decodes, so a thread waits only for its own wavefront's copies), decoded one stage
+//     ahead into a double-buffered MFMA B layout; the norms of the tile's 64 columns, all
+//     groups, are read once before the loop;
+//   - iteration t copies stage t + 3 into slot (t + 3) % 4, which no live stage holds
+//     (past the last stage the copied stage is clamped, so every wavefront issues the same
+//     4 copies per stage and `s_waitcnt vmcnt(8)` leaves exactly the two younger stages in
+//     flight), reads stage t's operands, waits for stage t + 1, decodes it, runs stage t's
+//     MFMAs and folds, and passes one barrier. The loop issues no other vector-memory
+//     instruction.
+constexpr int kCq4Stages = 4;
+constexpr int kCq4PipeWaves = 8;
+constexpr uint32_t kCq4NormsMax = 128;  // norm groups per column held in LDS
+
+struct Cq4PipeLds {
+    u32x4 a[kCq4Stages][kCq4Limbs][8][64];  // as Cq4MfmaStage::a, per stage
+    uint32_t braw[kCq4Stages][512];         // stage, thread: its packed word as copied
+    u32x4 b[2][2][2][4][64];                // stage parity, sub-group, codebook limb, 16-column tile, slot
+    uint16_t norms[kCq4NormsMax][kCq4Tile]; // group, tile column (fp16 bits)
+    uint32_t lut[16];
+};
+static_assert(sizeof(Cq4PipeLds) <= 160 * 1024, "LDS budget");
+
+// Slot of the decoded B entry for column j and word q within its 64-slot tile: 16 q + (j xor m(q)),
+// m = 0, 12, 4, 8. gfx950 serves 128-bit LDS accesses 16 lanes per cycle (in a half-wavefront, the
+// 4-lane chunks whose index has even parity together, then the odd ones), and two of those lanes
+// conflict when their addresses agree modulo 256 bytes. A decoding thread's 4-lane chunk holds one
+// column's 4 words and a cycle 4 columns, an MFMA reader's cycle 8 columns of two words: with
+// these masks both see 16 distinct 16-byte bank groups (plain j + 16 q conflicts 4-way on the writes).
+__device__ __forceinline__ int cq4_b_slot(int j, int q) { return 16 * q + (j ^ ((0x84C0 >> (4 * q)) & 0xF)); }
+
+__global__ __launch_bounds__(64 * kCq4PipeWaves) void cq4_gemm_pipe_kernel(Cq4View w, const uint16_t* __restrict__ xs,
+                                                                          uint16_t* __restrict__ c, uint32_t M,
+                                                                          uint32_t gs, uint32_t ng, uint32_t tiles_m) {
+    __shared__ Cq4PipeLds lds;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wid & 3, wn = wid >> 2;
+    const int j = lane & 15, q = lane >> 4;
+    const int K = static_cast<int>(w.K), N = static_cast<int>(w.N), Mi = static_cast<int>(M);
+    const int T = K / 64;
+    const int spg = static_cast<int>(gs) >> 5;
+    const int G = static_cast<int>(ng);
+    const int mt0 = static_cast<int>(blockIdx.x % tiles_m) * kCq4Tile;
+    const int nt0 = static_cast<int>(blockIdx.x / tiles_m) * kCq4Tile;
+    const int m0 = mt0 + 16 * wm, n0 = nt0 + 32 * wn;
+
+    // Activation-limb copy of this wavefront: 8-row block wid (row pairs 4 wid .. 4 wid + 3).
+    const uint16_t* asrc;
+    {
+        const int pair = 4 * wid + (lane >> 4);
+        const int row_t = 2 * pair + ((lane >> 3) & 1);
+        asrc = xs + static_cast<size_t>(min(mt0 + row_t, Mi - 1)) * T * (kCq4Limbs * 64) + 8 * ((lane & 7) ^ (pair & 7));
+    }
+    // Packed-index word of this thread: sub-group bu, tile column bc, word bw.
+    const int bu = tid >> 8, bc = (tid >> 2) & 63, bw = tid & 3;
+    const uint32_t* bsrc =
+        reinterpret_cast<const uint32_t*>(w.packed + static_cast<size_t>(min(nt0 + bc, N - 1)) * (K >> 1)) + bw;
+    const int blane = cq4_b_slot(bc & 15, bw);
+    const int bslot = cq4_b_slot(j, q);
+    const int pr = (16 * wm + j) >> 1;  // this lane's A row pair
+    const int arow = pr * 16 + 8 * (j & 1);
+
+    // Stage t's copies into stage slot st (past the last stage, t is clamped and st is not).
+    auto issue = [&](int t, int st) {
+#pragma unroll
+        for (int li = 0; li < kCq4Limbs; ++li)
+            __builtin_amdgcn_global_load_lds(asrc + static_cast<size_t>(t) * (kCq4Limbs * 64) + li * 64,
+                                             &lds.a[st][li][wid][0], 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(bsrc + 4 * (2 * t + bu), &lds.braw[st][64 * wid], 4, 0, 0);
+    };
+    auto decode = [&](int t) {
+        const int st = t & (kCq4Stages - 1), par = t & 1;
+        const uint32_t wd = lds.braw[st][tid];
+        uint32_t e[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) e[k] = lds.lut[(wd >> (4 * k)) & 0xFu];
+        u32x4 hi, lo;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            hi[i] = __builtin_amdgcn_perm(e[2 * i + 1], e[2 * i], 0x05040100u);  // low halves
+            lo[i] = __builtin_amdgcn_perm(e[2 * i + 1], e[2 * i], 0x07060302u);  // high halves
+        }
+        lds.b[par][bu][0][bc >> 4][blane] = hi;
+        lds.b[par][bu][1][bc >> 4][blane] = lo;
+    };
+    auto barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+
+    issue(0, 0);
+    issue(min(1, T - 1), 1);
+    issue(min(2, T - 1), 2);
+    // Codebook and norms with ordinary loads, after the copies are on their way.
+    if (tid < 16) {
+        const float v = half_bits_to_float(w.codebook[tid]);
+        const uint32_t hi = __float_as_uint(v) & 0xFFFF0000u;
+        const float lo = v - __uint_as_float(hi);  // exact, at most 3 significant bits
+        lds.lut[tid] = (hi >> 16) | (__float_as_uint(lo) & 0xFFFF0000u);
+    }
+    // two loads in flight per thread and pass (64 * G <= 8192 values: at most 8 passes)
+    for (int e0 = tid; e0 < kCq4Tile * G; e0 += 2 * 64 * kCq4PipeWaves) {
+        uint16_t v[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int e = min(e0 + 64 * kCq4PipeWaves * i, kCq4Tile * G - 1);
+            const int col = e / G, g = e - col * G;
+            v[i] = w.norms[static_cast<size_t>(min(nt0 + col, N - 1)) * G + g];
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int e = e0 + 64 * kCq4PipeWaves * i;
+            if (e < kCq4Tile * G) lds.norms[e % G][e / G] = v[i];
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();  // lut visible
+    decode(0);
+    barrier();
+
+    const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    double acc[2][4];
+#pragma unroll
+    for (int tn = 0; tn < 2; ++tn)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[tn][i] = 0.0;
+
+    for (int t = 0; t < T; ++t) {
+        issue(min(t + 3, T - 1), (t + 3) & (kCq4Stages - 1));
+        const int st = t & (kCq4Stages - 1), par = t & 1;
+        bf16x8 bh[2][2], bl[2][2], av[2][kCq4Limbs];
+        double nv[2][2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn) {
+                bh[u][tn] = __builtin_bit_cast(bf16x8, lds.b[par][u][0][wn * 2 + tn][bslot]);
+                bl[u][tn] = __builtin_bit_cast(bf16x8, lds.b[par][u][1][wn * 2 + tn][bslot]);
+            }
+            const int idx = arow + ((4 * u + q) ^ (pr & 7));
+#pragma unroll
+            for (int li = 0; li < kCq4Limbs; ++li) av[u][li] = __builtin_bit_cast(bf16x8, (&lds.a[st][li][0][0])[idx]);
+            const int g = (2 * t + u) / spg;
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn)
+                nv[u][tn] = static_cast<double>(half_bits_to_float(lds.norms[g][32 * wn + 16 * tn + j]));
+        }
+        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // this wavefront's copies of stage t + 1
+        decode(t + 1);  // past the last stage: rewrites an unread buffer from a clamped copy
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            f32x4_t P[2];
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn) {
+                const bf16x8* a3 = av[u];
+                f32x4_t r = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3[2], bl[u][tn], zero, 0, 0, 0);
+                r = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3[1], bl[u][tn], r, 0, 0, 0);
+                r = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3[2], bh[u][tn], r, 0, 0, 0);
+                r = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3[0], bl[u][tn], r, 0, 0, 0);
+                r = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3[1], bh[u][tn], r, 0, 0, 0);
+                P[tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3[0], bh[u][tn], r, 0, 0, 0);
+            }
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[tn][i] = fma(nv[u][tn], static_cast<double>(P[tn][i]), acc[tn][i]);
+        }
+        barrier();
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped copies past the last stage
+#pragma unroll
+    for (int tn = 0; tn < 2; ++tn) {
+        const int col = n0 + 16 * tn + j;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = m0 + 4 * q + i;
+            if (row < Mi && col < N) c[static_cast<size_t>(row) * N + col] = float_to_half_bits(static_cast<float>(acc[tn][i]));
+        }
+    }
+}
+
 bool cq4_uses_mfma(const Cq4View& w, uint32_t m) {
     const bool orth = (w.flags & kCq4FlagOrthogonal) != 0;
     const uint32_t gs = orth ? w.K : w.group_size;
@@ -567,8 +770,12 @@ hipError_t launch_cq4_matmul(const Cq4View& w, const uint16_t* a, uint32_t m, ui
     const bool inter = (w.flags & kCq4FlagInterleaved4Row) != 0;
     if (mfma) {
         const uint32_t tiles_m = (m + kCq4Tile - 1) / kCq4Tile, tiles_n = (w.N + kCq4Tile - 1) / kCq4Tile;
-        hipLaunchKernelGGL(cq4_gemm_mfma_kernel, dim3(tiles_m * tiles_n), dim3(256), 0, stream, w, xs, c, m, gs, ng,
-                           tiles_m);
+        if (ng <= kCq4NormsMax)
+            hipLaunchKernelGGL(cq4_gemm_pipe_kernel, dim3(tiles_m * tiles_n), dim3(64 * kCq4PipeWaves), 0, stream, w,
+                               xs, c, m, gs, ng, tiles_m);
+        else
+            hipLaunchKernelGGL(cq4_gemm_mfma_kernel, dim3(tiles_m * tiles_n), dim3(256), 0, stream, w, xs, c, m, gs,
+                               ng, tiles_m);
         return hipGetLastError();
     }
     if (m <= 4 && w.bits == 4 && gs % 8 == 0) {

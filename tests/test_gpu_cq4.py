@@ -91,14 +91,17 @@ def test_random_matrices(session, gpu, case):
 # M >= 32 with 4-bit LSB-packed indices, group sizes that are multiples of 32 and K % 64 == 0 run
 # on the MFMA kernel: ragged row and column tiles, one to several groups per row, signs,
 # permutation, both input-scale forms, the orthogonal basis, and the reference benchmark's 1024^3
-# shape; K = 96 (not a multiple of 64) at M = 48 stays on the other kernel.
+# shape; K = 96 (not a multiple of 64) at M = 48 stays on the other kernel. Up to 128 norm groups
+# per column the pipelined MFMA kernel runs, beyond that the single-stage one.
 MFMA_CASES = [dict(bits=4, K=512, N=200, group_size=128, m=70),
               dict(bits=4, K=96, N=50, group_size=32, m=48),
               dict(bits=4, K=1024, N=96, group_size=256, signs=True, perm=True, scale="scale", m=33),
               dict(bits=4, K=128, N=72, group_size=128, orthogonal=True, m=40),
               dict(bits=4, K=256, N=130, group_size=32, m=64),
               dict(bits=4, K=512, N=64, group_size=64, scale="none", m=129),
-              dict(bits=4, K=1024, N=1024, group_size=128, m=1024)]
+              dict(bits=4, K=1024, N=1024, group_size=128, m=1024),
+              dict(bits=4, K=4096, N=72, group_size=32, m=40),    # 128 norm groups: the most held in LDS
+              dict(bits=4, K=8192, N=40, group_size=32, m=36)]    # 256 groups: the single-stage kernel
 
 
 @pytest.mark.parametrize("case", range(len(MFMA_CASES)))
