@@ -114,12 +114,39 @@ __global__ __launch_bounds__(256) void cq4_transform_hadamard_wave_kernel(Cq4Vie
     if (pair >= pairs) return;  // whole wavefronts only: no cross-lane exchange is cut short
     const uint32_t g = pair % w.num_groups;
     const size_t base = static_cast<size_t>(pair / w.num_groups) * w.K + static_cast<size_t>(g) * gs;
+    // Every load of the wavefront is issued before any is used (one memory round trip): an
+    // absent optional array is read from `a` instead (in bounds: its first K values) and the
+    // value ignored, so only the permutation, when present, adds a branch.
+    uint16_t ar[E], sr[E];
+    int8_t ls[E], rs[E];
+    uint32_t src[E];
+    const uint16_t* srow = w.input_scale_recip ? w.input_scale_recip : (w.input_scale ? w.input_scale : a);
+    const int8_t* lsp = w.left_signs ? w.left_signs : reinterpret_cast<const int8_t*>(a);
+    const int8_t* rsp = w.right_signs ? w.right_signs : reinterpret_cast<const int8_t*>(a);
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+        ar[i] = a[base + lane + 64 * i];
+        sr[i] = srow[g * gs + lane + 64 * i];
+        ls[i] = lsp[lane + 64 * i];
+    }
+    if (w.permutation) {
+        // an out-of-range entry is masked into the group (the host entry point rejects it)
+#pragma unroll
+        for (int i = 0; i < E; ++i) src[i] = w.permutation[lane + 64 * i] & (gs - 1);
+    } else {
+#pragma unroll
+        for (int i = 0; i < E; ++i) src[i] = lane + 64 * i;
+    }
+#pragma unroll
+    for (int i = 0; i < E; ++i) rs[i] = rsp[src[i]];
     float v[E];
 #pragma unroll
     for (int i = 0; i < E; ++i) {
-        const uint32_t k = lane + 64 * i;
-        const float sign = w.left_signs ? static_cast<float>(w.left_signs[k]) : 1.0f;
-        v[i] = half_bits_to_float(a[base + k]) * input_recip(w, g * gs + k) * sign;
+        // input_recip's value: the reciprocal as given, or 1 / scale, or 1
+        const float r = w.input_scale_recip ? half_bits_to_float(sr[i])
+                                            : (w.input_scale ? 1.0f / half_bits_to_float(sr[i]) : 1.0f);
+        const float sign = w.left_signs ? static_cast<float>(ls[i]) : 1.0f;
+        v[i] = half_bits_to_float(ar[i]) * r * sign;
     }
     for (uint32_t h = 1; h < 64; h <<= 1) {  // strides 1 .. 32 across lanes
         const bool upper = (lane & h) != 0;
@@ -142,14 +169,16 @@ __global__ __launch_bounds__(256) void cq4_transform_hadamard_wave_kernel(Cq4Vie
 #pragma unroll
     for (int i = 0; i < E; ++i) {
         const uint32_t j = lane + 64 * i;
-        const uint32_t src = w.permutation ? (w.permutation[j] & (gs - 1)) : j;
-        float x = 0.0f;
+        float x = v[i];  // no permutation: element j is this lane's own
+        if (w.permutation) {  // uniform
+            x = 0.0f;
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-            const float t = __shfl(v[e], static_cast<int>(src & 63));
-            x = (src >> 6) == static_cast<uint32_t>(e) ? t : x;
+            for (int e = 0; e < E; ++e) {
+                const float t = __shfl(v[e], static_cast<int>(src[i] & 63));
+                x = (src[i] >> 6) == static_cast<uint32_t>(e) ? t : x;
+            }
         }
-        const float sign = w.right_signs ? static_cast<float>(w.right_signs[src]) : 1.0f;
+        const float sign = w.right_signs ? static_cast<float>(rs[i]) : 1.0f;
         store_code(out, xs, w.K, pair / w.num_groups, g * gs + j, x * inv * sign);
     }
 }
@@ -679,24 +708,39 @@ __global__ __launch_bounds__(64 * kCq4PipeWaves) void cq4_gemm_pipe_kernel(Cq4Vi
         }
         asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // this wavefront's copies of stage t + 1
         decode(t + 1);  // past the last stage: rewrites an unread buffer from a clamped copy
+        // Four independent chains (sub-group u, column tile tn), interleaved step by step; each
+        // chain adds its six limb products smallest first.
+        f32x4_t P[2][2];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            f32x4_t P[2];
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int tn = 0; tn < 2; ++tn) {
-                const bf16x8* a3 = av[u];
-                f32x4_t r = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3[2], bl[u][tn], zero, 0, 0, 0);
-                r = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3[1], bl[u][tn], r, 0, 0, 0);
-                r = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3[2], bh[u][tn], r, 0, 0, 0);
-                r = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3[0], bl[u][tn], r, 0, 0, 0);
-                r = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3[1], bh[u][tn], r, 0, 0, 0);
-                P[tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3[0], bh[u][tn], r, 0, 0, 0);
-            }
+            for (int tn = 0; tn < 2; ++tn) P[u][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[u][2], bl[u][tn], zero, 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn) P[u][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[u][1], bl[u][tn], P[u][tn], 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn) P[u][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[u][2], bh[u][tn], P[u][tn], 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn) P[u][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[u][0], bl[u][tn], P[u][tn], 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn) P[u][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[u][1], bh[u][tn], P[u][tn], 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn) P[u][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[u][0], bh[u][tn], P[u][tn], 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
             for (int tn = 0; tn < 2; ++tn)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) acc[tn][i] = fma(nv[u][tn], static_cast<double>(P[tn][i]), acc[tn][i]);
-        }
+                for (int i = 0; i < 4; ++i) acc[tn][i] = fma(nv[u][tn], static_cast<double>(P[u][tn][i]), acc[tn][i]);
         barrier();
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped copies past the last stage
