@@ -34,6 +34,19 @@
  *   words). w_scales is float[N][K/32]; dequant(k, n) = v(k, n) * w_scales[n*(K/32) + k/32].
  *   x is float[M][K] row-major; y is float[M][N] row-major.
  *   y[m][n] = sum_k x[m][k] * dequant(k, n)   (fp32 inputs, fp32 output).
+ *
+ * Accuracy, as max |y - ref| / max(1, |ref|) against the double-precision
+ * reference (test_q4gemm.cpp:102-119, metric of test_q4gemm.cpp:380):
+ *   - m <= 32 (fp32 FMA / fp32 MFMA paths): <= 1e-5.
+ *   - m > 32 (bf16 MFMA on x split exactly into three bf16 limbs; every product
+ *     exact, one fp32 rounding per 32-value group sum, groups summed in double):
+ *     <= 1e-5 on the reference's KAT (256^3, test_q4gemm.cpp:40-49) and on the
+ *     documented workload shapes; stated tolerance 2.5e-5 in general (inputs whose
+ *     group partial sums dwarf the output they sum to, e.g. unit-range x and
+ *     scales at K = 1024 near zero outputs).
+ *   - A non-finite x gives IEEE's result for x itself, as the reference does: every
+ *     output of that row is non-finite, NaN where inf meets a zero nibble, opposite
+ *     infinities meet or a NaN enters, the signed infinity otherwise.
  */
 #ifndef SPACESLUG_RUNTIME_ABI_H
 #define SPACESLUG_RUNTIME_ABI_H
