@@ -75,6 +75,11 @@ struct DeviceState {
     hipEvent_t ws_done = nullptr;
     hipStream_t ws_stream = nullptr;
     bool ws_used = false;
+    // Device buffers of the synchronous host-pointer calls (grow-only, reused call after call),
+    // and the lock a call holds while it uses them.
+    void* staging = nullptr;
+    size_t staging_bytes = 0;
+    std::mutex staging_mutex;
 };
 
 // Fixed table: setting up a device's state allocates nothing on the host either.
@@ -131,20 +136,42 @@ void* device_workspace(DeviceState& d, size_t bytes) {
     return d.workspace;
 }
 
-// One device allocation carved into 256-byte aligned slices; freed on scope exit.
+// Largest staging the device keeps between host-pointer calls; a call needing more (a one-off
+// weight upload or quantization) allocates for itself and frees on return.
+constexpr size_t kStagingKeepBytes = size_t{256} << 20;
+
+// The device buffers of one synchronous host-pointer call, carved into 256-byte aligned slices.
+// Up to kStagingKeepBytes they are the device's grow-only staging buffer, so a steady sequence of
+// such calls (the per-token projections on resident weights, spaceslug_q4gemm_run) allocates
+// nothing after the first: every host-pointer call returns only after its last copy back, so the
+// buffer is idle between calls. The device's staging lock is held for the call.
 class StagingArena {
 public:
-    explicit StagingArena(const std::vector<size_t>& sizes) {
+    explicit StagingArena(const std::vector<size_t>& sizes) : dev_(current_device()), lock_(dev_.staging_mutex) {
         size_t total = 0;
         for (size_t s : sizes) {
             offsets_.push_back(total);
             total += (s + 255) & ~static_cast<size_t>(255);
         }
         if (total == 0) total = 256;
-        check(hipMalloc(&base_, total), "hipMalloc (staging)");
+        if (total > kStagingKeepBytes) {
+            check(hipMalloc(&own_, total), "hipMalloc (staging)");
+            base_ = own_;
+            return;
+        }
+        if (dev_.staging_bytes < total) {
+            if (dev_.staging) {
+                check(hipFree(dev_.staging), "hipFree (staging)");
+                dev_.staging = nullptr;
+                dev_.staging_bytes = 0;
+            }
+            check(hipMalloc(&dev_.staging, total), "hipMalloc (staging)");
+            dev_.staging_bytes = total;
+        }
+        base_ = dev_.staging;
     }
     ~StagingArena() {
-        if (base_) (void)hipFree(base_);
+        if (own_) (void)hipFree(own_);
     }
     StagingArena(const StagingArena&) = delete;
     StagingArena& operator=(const StagingArena&) = delete;
@@ -154,6 +181,9 @@ public:
     }
 
 private:
+    DeviceState& dev_;
+    std::lock_guard<std::mutex> lock_;
+    void* own_ = nullptr;
     void* base_ = nullptr;
     std::vector<size_t> offsets_;
 };

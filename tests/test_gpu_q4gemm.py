@@ -321,6 +321,24 @@ def test_weight_handle(session, oracle, gpu):
             check(oracle, w.run(x, m), oracle.q4gemm_packed(x, c.packed, c.scales), label=f"handle m={m}")
 
 
+def test_host_calls_reuse_staging_across_sizes(session, oracle, gpu):
+    """The host-pointer calls share one grow-only device staging buffer: calls that grow it, shrink
+    back, switch paths (GEMV, small M, wide, LoRA) and mix with the weight handle all stay exact."""
+    note("host staging reuse")
+    n, k = 260, 1024
+    c = make_case(300, n, k)
+    la, lb = lora_factors(k, n, 4)
+    with session.create_q4_weight(c.packed, c.scales, n, k) as w:
+        for m in (1, 64, 2, 300, 5, 40, 1):
+            x = c.x[:m]
+            want = oracle.q4gemm_packed(x, c.packed, c.scales)
+            check(oracle, session.q4gemm_values(x, c.packed, c.scales, m, n, k), want, label=f"host m={m}")
+            check(oracle, w.run(x, m), want, label=f"handle m={m}")
+            if m in (64, 5):
+                got = session.q4gemm_lora_values(x, c.packed, c.scales, la, lb, m, n, k, 4, 2.0)
+                check(oracle, got, oracle.q4gemm_lora(x, c.packed, c.scales, la, lb, 2.0), label=f"lora m={m}")
+
+
 def test_sgemm(session, gpu):
     note("sgemm")
     rng = np.random.default_rng(0)
