@@ -675,19 +675,20 @@ __device__ __forceinline__ void lora_t_block(const float* __restrict__ x, const 
     }
 }
 
-// One launch that prepares a call's GEMM: blocks [0, split_blocks) split x into bf16
-// limbs (split_x_block; none when the GEMM reads fp32 x), the rest compute the LoRA T
-// partials (lora_t_block, grid tiles_m_t x tiles_r x t_splits). Both only read x.
+// One launch that prepares a call's GEMM: the first lora_blocks workgroups compute the LoRA T
+// partials (lora_t_block, grid tiles_m_t x tiles_r x t_splits), the rest split x into bf16
+// limbs (split_x_block; none when the GEMM reads fp32 x). Both only read x. The T workgroups
+// come first because each runs a long dependent chain (all of its loads, then its MFMAs): started
+// last, behind the many short split workgroups, they set the launch's end.
 __global__ __launch_bounds__(256) void prep_kernel(const float* __restrict__ x, uint16_t* __restrict__ xs, int M,
-                                                   int K, int KB, int split_blocks, const float* __restrict__ la,
+                                                   int K, int KB, int lora_blocks, const float* __restrict__ la,
                                                    float* __restrict__ tpart, int R, int tiles_m_t, int tiles_r) {
     const int b = static_cast<int>(blockIdx.x);
-    if (b < split_blocks) {
-        split_x_block(x, xs, M, K, KB, b);
+    if (b >= lora_blocks) {
+        split_x_block(x, xs, M, K, KB, b - lora_blocks);
         return;
     }
-    const int t = b - split_blocks;
-    lora_t_block(x, la, tpart, M, K, R, t % tiles_m_t, (t / tiles_m_t) % tiles_r, t / (tiles_m_t * tiles_r));
+    lora_t_block(x, la, tpart, M, K, R, b % tiles_m_t, (b / tiles_m_t) % tiles_r, b / (tiles_m_t * tiles_r));
 }
 
 // Small-M GEMM (M <= 32, K % 128 == 0) with no K-split partials in memory: a
@@ -1019,7 +1020,7 @@ hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float*
         const int lora_blocks = rank ? tiles_m_t * tiles_r * plan.t_splits : 0;
         if (split_blocks + lora_blocks > 0) {
             hipLaunchKernelGGL(prep_kernel, dim3(static_cast<unsigned>(split_blocks + lora_blocks)), dim3(256), 0,
-                               stream, x, xs, mm, kk, KB, split_blocks, la, tpart, rr, tiles_m_t, tiles_r);
+                               stream, x, xs, mm, kk, KB, lora_blocks, la, tpart, rr, tiles_m_t, tiles_r);
             const hipError_t pe = hipGetLastError();
             if (pe != hipSuccess) return pe;
         }
