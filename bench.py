@@ -20,7 +20,7 @@ least 15 HIP-event-timed iterations after warm-up:
   - "roofline": achieved GB/s of the GEMV kernel vs MI355X's 8 TB/s HBM peak;
   - "prefill": the M=2048, K=4096, N=14336 GEMM in TFLOP/s (2*M*N*K / time, the second half of the
     headline metric). Its roofline is the matrix instruction the kernel runs: above 32 rows that is
-    v_mfma_f32_16x16x32_bf16 on x split exactly into three bf16 limbs, so the matrix core executes
+    v_mfma_f32_32x32x16_bf16 on x split exactly into three bf16 limbs, so the matrix core executes
     3 * 2*M*N*K bf16 flops, priced against the 2.5 PFLOP/s dense bf16 peak (the fp32-equivalent rate
     and the 157.3 TFLOP/s fp32 MFMA peak are given beside it); at 32 rows or fewer the kernels run
     v_mfma_f32_16x16x4_f32, priced against 157.3 TFLOP/s;
@@ -71,7 +71,7 @@ def gemm_roofline(m: int, n: int, k: int, seconds_per_call: float) -> dict:
     tf = 2.0 * m * n * k / seconds_per_call / 1e12
     if m >= WIDE_MIN_ROWS:
         achieved = BF16_LIMBS * tf
-        return {"bound": "mfma", "instruction": "v_mfma_f32_16x16x32_bf16 (x as 3 exact bf16 limbs)",
+        return {"bound": "mfma", "instruction": "v_mfma_f32_32x32x16_bf16 (x as 3 exact bf16 limbs)",
                 "achieved": round(achieved, 2), "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / BF16_MFMA_PEAK_TFLOPS, 4), "fp32_equivalent_tflops": round(tf, 2),
                 "fp32_mfma_peak": FP32_MFMA_PEAK_TFLOPS}

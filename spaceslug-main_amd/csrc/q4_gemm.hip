@@ -6,18 +6,19 @@
 // Replaces q4gemm.comp:61-175 (64x64 tile, LDS-staged dequantised B, 4x4 FMA
 // micro-tile per thread) with a CDNA4 design on the matrix cores: the two
 // small-M kernels on v_mfma_f32_16x16x4_f32, the wide kernel on
-// v_mfma_f32_16x16x32_bf16 with x split exactly into three bf16 limbs.
+// v_mfma_f32_32x32x16_bf16 with x split exactly into three bf16 limbs.
 // Common to all three:
-//   - per 32-value scale group, lane (j = l%16, q = l/16) feeds the MFMA K slot
-//     q with k = 8q .. 8q + 7, so its B operands for column j are the 8 nibbles
-//     of ONE 32-bit word of the packed column (word q of the group's 16 bytes)
-//     and its A operands are 8 consecutive values of row j. Weights are decoded
-//     to v / 16 (v_cvt_off_f32_i4, exact; the factor 16 joins the scale);
+//   - per 32-value scale group, each lane feeds the MFMA K slots with 8
+//     consecutive K values, so its B operands for one column are the 8 nibbles
+//     of ONE 32-bit word of the packed column and its A operands are 8
+//     consecutive values of one row. Weights are decoded to v / 16
+//     (v_cvt_off_f32_i4, exact; the factor 16 joins the scale or multiplies the
+//     float64 sums at the store);
 //   - every product x * v / 16 is exact in fp32; the MFMA accumulates
 //     P = sum x * v / 16 over one group in fp32 from zero, and the group is
-//     folded straight into a float64 accumulator as 16 s * P. Scale application
+//     folded straight into a float64 accumulator as s * P. Scale application
 //     moves out of the inner loop, the long K sum is carried in double, and the
-//     one fp32 rounding of each group's sum is the only error left;
+//     fp32 roundings of each group's sum are the only error left;
 //   - large grids are XCD-aware: workgroup ids are remapped so each of the 8
 //     XCDs (one L2 each) walks a contiguous band of output tiles, sharing A
 //     rows and weight columns within its L2;
@@ -293,54 +294,53 @@ __global__ __launch_bounds__(256) void split_x_kernel(const float* __restrict__ 
     split_x_block(x, xs, M, K, KB, blockIdx.x);
 }
 
-// Wide tile for M > 32 (prefill, LoRA projections): 128 x 128 outputs per
-// workgroup of 8 wavefronts, two per SIMD, each wavefront 32 x 64 outputs (2 x 4
-// MFMA tiles). The matrix instruction is v_mfma_f32_16x16x32_bf16, fed with x as
-// three exact bf16 limbs (split_x_kernel) and the weights as bf16 v/16 (exact):
-// every product is exact in fp32 and each 32-value group's sum P = sum x * v/16 is
-// accumulated in fp32 by three chained MFMAs (smallest limb first), and the group is
-// folded into float64 as acc += 16 s * P (one fp32 rounding per group sum is the
-// whole error: 6.3e-6 on the reference KAT, <= 3.7e-6 on the workload shapes).
-// A 32 x 64 wavefront tile keeps the LDS operand reads per MFMA lowest for three
-// x limbs per weight (10 KiB per group and wavefront) at 2 wavefronts per SIMD
-// (the float64 accumulators need 64 VGPRs per wavefront).
-// Lane (j = l%16, q = l/16) of a 16x16x32 MFMA holds A[row j][k = 8q .. 8q+7] and
-// B[k = 8q .. 8q+7][column j] (8 bf16 each), and result rows 4q .. 4q+3 of column
-// j. Every operand reaches LDS by global_load_lds (no VGPRs, no register waits):
-//   - x limbs, one 32-value group per stage, kWideStages buffers (3 groups in
-//     flight behind the one computed): 3 limbs x 128 rows x 32 values (24 KiB);
-//     wavefront w copies rows 16w .. 16w+15 of each limb, one 1 KiB instruction per
-//     limb. Row r's 16-byte chunk c of a 16-row set sits at chunk
-//     16 (r>>2) + 4 (r&3) + (c ^ ((r>>2) & 2)): gfx950 serves a 128-bit LDS read 16
-//     lanes per cycle, the 4-lane chunks of a half-wavefront whose chunk index has
-//     even parity (lanes 0-3, 12-15, 20-23, 24-27) in one cycle and odd parity in
-//     the other, and two of those lanes conflict when their addresses agree modulo
-//     256 bytes; this placement gives each cycle's 16 MFMA-operand reads 16
-//     distinct 16-byte bank groups (measured: no bank-conflict cycles);
-//   - packed weights and scales, four groups at a time (a "quad"): lane l of
-//     wavefront w copies the 16 bytes of group 4Q + (l >> 4) of tile column
-//     16w + (l & 15), and that group's scale. A column's 4 lanes read 64 contiguous
-//     bytes, so an instruction touches 16 lines where one group at a time touched as
-//     many lines for a quarter of the bytes, and the per-column scales (512 bytes
-//     apart in [N][K/32]) cost 16 lines per instruction instead of 64;
-//   - one stage ahead of its use, each thread decodes one packed word of the
-//     stage's group (the one its own wavefront copied) into the MFMA B layout
-//     (bf16 v/16, 8 KiB per group), so every wavefront reads its B operands as
-//     linear 1 KiB runs.
-// Iteration s copies stage s + 3, waits for stage s + 1 (s_waitcnt vmcnt with the
-// exact count of copies issued after it: 3 per stage, 2 more on quad boundaries;
-// measured wait ~12 cycles per group, so three stages in flight hide the copies),
-// decodes it, passes one workgroup barrier and reads stage s + 1's operands into
-// registers while stage s's MFMAs run. Copies past the end of the K range are
-// clamped to its last group (never computed), so the counts hold everywhere.
+// Wide tile for M > 32 (prefill, LoRA projections): 128 x 128 outputs per workgroup of 8
+// wavefronts, two per SIMD, each wavefront 32 x 64 outputs (two 32 x 32 MFMA tiles). The
+// matrix instruction is v_mfma_f32_32x32x16_bf16, fed with x as three exact bf16 limbs
+// (split_x_block) and the weights as bf16 v/16 (exact): every product is exact in fp32, each
+// 32-value group's sum P = sum x * v/16 is accumulated in fp32 by six chained MFMAs per tile
+// (limb 2, 1, 0, smallest first, each over the group's two 16-value halves), and the group is
+// folded into float64 as acc += s * P; the factor 16 multiplies the float64 sums once, at the
+// store (exact). One fp32 rounding per MFMA is the whole error, and the two of limb 0 dominate
+// it: 4.5e-6 emulated on the reference KAT against 4.3e-6 for one 32-value MFMA per limb.
+// Why 32 x 32 x 16: a gfx950 SIMD executes VALU instructions under its MFMAs, from either of
+// its wavefronts, but only about 2 per 16 x 16 x 32 MFMA (16 matrix-core cycles) against about
+// 6 per 32 x 32 x 16 MFMA (32 cycles); the float64 fold costs 2 VALU instructions per output
+// and group, the same number per matrix-core cycle for both shapes, so only this shape keeps
+// the fold (66 instructions per group and wavefront) inside the shadow of its 12 MFMAs.
+// Lane l of a 32x32x16 MFMA holds A[row l%32][k = 8(l/32) .. +7] and B[k = 8(l/32) .. +7]
+// [column l%32] (8 bf16 each), and result element v is row 8(v/4) + 4(l/32) + v%4 of
+// column l%32, so every result a lane holds is in one column and needs one scale. Every
+// operand reaches LDS by global_load_lds (no VGPRs, no register waits):
+//   - x limbs, one 32-value group per stage, kWideStages buffers (the stage being read into
+//     registers and 3 in flight): 3 limbs x 128 rows x 32 values (24 KiB); wavefront w copies
+//     rows 16w .. 16w+15 of each limb, one 1 KiB instruction per limb. Row r's 16-byte chunk c
+//     (8 values) sits at chunk c ^ ((r >> 2) & 3) of the row's 64 bytes: gfx950 serves a 128-bit LDS read
+//     16 lanes per cycle, the 4-lane chunks of a half-wavefront whose chunk index has even
+//     parity (lanes 0-3, 12-15, 20-23, 24-27) in one cycle and odd parity in the other, and two
+//     of those lanes conflict when their addresses agree modulo 256 bytes; an operand read
+//     (32 rows, one chunk per half-wavefront) then touches 16 distinct 16-byte bank groups in
+//     each cycle;
+//   - packed weights and scales, four groups at a time (a "quad"): lane l of wavefront w copies
+//     the 16 bytes of group 4Q + (l >> 4) of tile column 16w + (l & 15), and that group's scale.
+//     A column's 4 lanes read 64 contiguous bytes, and the per-column scales (512 bytes apart in
+//     [N][K/32]) cost 16 lines per instruction;
+//   - one stage ahead of its use, each thread decodes one packed word of the stage's group (one
+//     its own wavefront copied) into the MFMA B layout (bf16 v/16, 8 KiB per group: 32-column
+//     tile, 16-value half, lane), so every wavefront reads its B operands as linear 1 KiB runs.
+// Iteration s passes one workgroup barrier (publishing stage s + 1), copies stage s + 4 into the
+// buffers stage s was read from, reads stage s + 1's operands into registers spread over the
+// group's MFMAs, waits for stage s + 2 (s_waitcnt vmcnt with the exact count of copies issued
+// after it: 3 per stage, 2 more on quad boundaries) and decodes it. Copies past the end of the K
+// range are clamped to its last group (never computed), so the counts hold everywhere.
 constexpr int kWideStages = 4;
 constexpr int kWideWavesPerTile = 8;
 
 struct WideLds {
-    u32x4 a[kWideStages][kLimbs][8][64];  // stage, limb, 16-row set, swizzled 16-byte chunk
-    u32x4 b[2][8][64];                    // stage parity, 16-column tile, lane slot j + 16 q
-    u32x4 braw[2][8][64];                 // quad parity, wavefront, lane: 16 packed bytes as copied
-    float s[2][8][64];                    // quad parity, wavefront, lane: one scale as copied
+    u32x4 a[kWideStages][kLimbs][128][4];  // stage, limb, tile row, swizzled 16-byte chunk
+    u32x4 b[2][4][2][64];                  // stage parity, 32-column tile, 16-value half, lane
+    u32x4 braw[2][8][64];                  // quad parity, wavefront, lane: 16 packed bytes as copied
+    float s[2][8][64];                     // quad parity, wavefront, lane: one scale as copied
 };
 
 // Vector-memory instructions issue(t) adds per wavefront.
@@ -351,25 +351,45 @@ __host__ __device__ constexpr int wide_inflight(int first, int count) {
     return count == 0 ? 0 : wide_copies(first) + wide_inflight(first + 1, count - 1);
 }
 
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// Tile order of the wide kernel: XCD-contiguous runs as in xcd_tile, over a linear order that
+// walks bands of kWideBandRows tile rows, each band column by column with its rows fastest. The
+// 32 CUs of an XCD then hold 2 tile rows x 16 tile columns at a time, whose operands per group
+// (2 x 24 KiB of x limbs, 16 x 2.5 KiB of weights and scales) are a quarter of those of 16 tile
+// rows x 2 columns: the x limbs of every row of the matrix, streamed from beyond the XCD's L2
+// once per column pair.
+constexpr int kWideBandRows = 2;
+__device__ __forceinline__ void wide_tile(int tiles_m, int tiles_n, int& tm, int& tn) {
+    const int total = tiles_m * tiles_n;
+    const int id = blockIdx.x;
+    int lin = id;
+    if (total >= 64 && (total & 7) == 0) lin = (id & 7) * (total >> 3) + (id >> 3);
+    const int band = lin / (kWideBandRows * tiles_n);
+    const int within = lin - band * kWideBandRows * tiles_n;
+    const int h = min(kWideBandRows, tiles_m - kWideBandRows * band);  // the last band may be shorter
+    tn = within / h;
+    tm = kWideBandRows * band + within % h;
+}
+
 __global__ __launch_bounds__(512) void q4_gemm_wide_kernel(const uint16_t* xs, const uint32_t* wq, const float* ws,
                                                           float* __restrict__ out, int M, int N, int K,
                                                           int tiles_m, int tiles_n, int groups_per_split,
                                                           const float* __restrict__ tpart, int t_splits,
                                                           const float* __restrict__ lb, int R, float lscale) {
-    constexpr int WM = 2, WN = 4;
     __shared__ WideLds lds;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wid & 3;
-    const int wn = wid >> 2;
-    const int j = lane & 15;
-    const int q = lane >> 4;
+    const int wm = wid & 3;   // rows 32 wm .. 32 wm + 31 of the tile
+    const int wn = wid >> 2;  // columns 64 wn .. 64 wn + 63 of the tile
+    const int col32 = lane & 31;
+    const int half = lane >> 5;
     const int G = K >> 5;
     const int KB = (G + 1) >> 1;
 
     int tile_m, tile_n;
-    xcd_tile(tiles_m, tiles_n, tile_m, tile_n);
+    wide_tile(tiles_m, tiles_n, tile_m, tile_n);
     const int mt0 = tile_m * 128, nt0 = tile_n * 128;
     const int m0 = mt0 + wm * 32;
     const int n0 = nt0 + wn * 64;
@@ -377,18 +397,16 @@ __global__ __launch_bounds__(512) void q4_gemm_wide_kernel(const uint16_t* xs, c
     const int g_end = min(G, g_begin + groups_per_split);
     const int n_groups = g_end - g_begin;
 
-    // x-limb copy of this wavefront: rows 16 wid .. 16 wid + 15 of the tile, lane -> (row, chunk).
-    const uint16_t* asrc;
-    {
-        const int b = lane >> 4;
-        const int r = 4 * b + ((lane >> 2) & 3);
-        const int c = (lane & 3) ^ (b & 2);
-        asrc = xs + static_cast<size_t>(min(mt0 + 16 * wid + r, M - 1)) * KB * (kLimbs * 64) + 8 * c;
-    }
-    // Quad copies: tile column 16 wid + j, group 4Q + q of the quad.
-    const int qcol = min(nt0 + 16 * wid + j, N - 1);
+    // x-limb copy of this wavefront: rows 16 wid .. 16 wid + 15 of the tile; lane i fills chunk
+    // slot i & 3 of row 16 wid + (i >> 2), which holds logical chunk (i & 3) ^ ((i >> 4) & 3).
+    const uint16_t* asrc =
+        xs + static_cast<size_t>(min(mt0 + 16 * wid + (lane >> 2), M - 1)) * KB * (kLimbs * 64) +
+        8 * ((lane & 3) ^ ((lane >> 4) & 3));
+    // Quad copies: tile column 16 wid + (lane & 15), group 4Q + (lane >> 4) of the quad.
+    const int qcol = min(nt0 + 16 * wid + (lane & 15), N - 1);
     const u32x4* bsrc = reinterpret_cast<const u32x4*>(wq + static_cast<size_t>(qcol) * (K >> 3));
     const float* ssrc = ws + static_cast<size_t>(qcol) * G;
+    const int qg = lane >> 4;
 
     // Copies of stage t of this split (clamped into it).
     auto issue = [&](int t) {
@@ -396,157 +414,184 @@ __global__ __launch_bounds__(512) void q4_gemm_wide_kernel(const uint16_t* xs, c
         const uint16_t* src = asrc + static_cast<size_t>(g >> 1) * (kLimbs * 64) + 32 * (g & 1);
 #pragma unroll
         for (int li = 0; li < kLimbs; ++li)
-            __builtin_amdgcn_global_load_lds(src + li * 64, &lds.a[t % kWideStages][li][wid][0], 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(src + li * 64, &lds.a[t % kWideStages][li][16 * wid][0], 16, 0, 0);
         if (t % 4 == 0) {  // uniform
-            const int gq = g_begin + min(t + q, n_groups - 1);
+            const int gq = g_begin + min(t + qg, n_groups - 1);
             const int qb = (t >> 2) & 1;
             __builtin_amdgcn_global_load_lds(bsrc + gq, &lds.braw[qb][wid][0], 16, 0, 0);
             __builtin_amdgcn_global_load_lds(ssrc + gq, &lds.s[qb][wid][0], 4, 0, 0);
         }
     };
-    // Decode of stage t's group: lane (j, q) of wavefront w turns word q of tile column 16w + j
-    // (copied by this wavefront) into b[t & 1][w][lane]; 64 lanes read 64 distinct banks.
-    auto commit = [&](int t) {
-        const uint32_t* raw = reinterpret_cast<const uint32_t*>(&lds.braw[(t >> 2) & 1][wid][j + 16 * (t & 3)]);
-        lds.b[t & 1][wid][lane] = nibbles_bf16_16th(raw[q]);
+    // Decode of stage t's group: lane (j = lane & 15, q = lane >> 4) of wavefront w turns word q
+    // of tile column c = 16w + j (copied by this wavefront) into the B slot of 32-column tile
+    // c >> 5, half q >> 1, lane (c & 31) + 32 (q & 1).
+    const int dj = lane & 15, dq = lane >> 4;
+    const int dslot = 16 * (wid & 1) + dj + 32 * (dq & 1);
+    auto read_raw = [&](int t) {
+        return reinterpret_cast<const uint32_t*>(&lds.braw[(t >> 2) & 1][wid][dj + 16 * (t & 3)])[dq];
     };
+    auto write_b = [&](int t, uint32_t raw) { lds.b[t & 1][wid >> 1][dq >> 1][dslot] = nibbles_bf16_16th(raw); };
     // The workgroup barrier without the fence __syncthreads() adds: that fence waits for every
     // outstanding copy (vmcnt(0)), including the stages still in flight. The copies a stage needs
     // are waited for explicitly before it; this wavefront's LDS reads and writes are waited for here.
     auto barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
-    double acc[WM][WN][4];
+    double acc[2][16];
 #pragma unroll
-    for (int tm = 0; tm < WM; ++tm)
+    for (int tn = 0; tn < 2; ++tn)
 #pragma unroll
-        for (int tn = 0; tn < WN; ++tn)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[tm][tn][i] = 0.0;
+        for (int v = 0; v < 16; ++v) acc[tn][v] = 0.0;
 
-    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-    // Per group and wavefront: 24 MFMAs (2 x 4 tiles x 3 limbs) and the fold of the previous
-    // group's 32 sums into float64 (72 VALU operations). On gfx950 a wavefront's VALU work
-    // overlaps the matrix core only while that wavefront's own MFMA executes (the other
-    // wavefront of the SIMD waits), so the group is laid out by hand as 24 "windows", each
-    // one MFMA followed by three fold operations of the previous group, with the stage
-    // pipeline's copies, decode, barrier and operand reads placed in the windows too;
-    // sched_barrier keeps the compiler from regrouping them.
-    struct OpsA {
-        bf16x8 a[WM][kLimbs];
-    };
+    f32x16 zero16;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) zero16[v] = 0.0f;
+    // Operands: A (limb, half) of limbs 2 and 1 for the group being computed, read one stage ahead
+    // once the MFMAs that use each register have issued; limb 0's A and B (tile, half)
+    // double-buffered, so every read of the next stage issues by window 9 and has landed when the
+    // next group starts; a group's sums and scales.
     struct OpsB {
-        bf16x8 b[WN];
-        float s[WN];
+        bf16x8 b[2][2];
     };
     struct Sums {
-        f32x4 p[WM][WN];
-        float s[WN];
+        f32x16 p[2];
+        float s[2];
     };
-    const int ch = 16 * (j >> 2) + 4 * (j & 3) + (q ^ ((j >> 2) & 2));
-    auto read_a = [&](OpsA& o, int t, int tm, int li) {
-        o.a[tm][li] = __builtin_bit_cast(bf16x8, lds.a[t & 3][li][2 * wm + tm][ch]);
+    const int arow = 32 * wm + col32;
+    const int pch0 = (0 + half) ^ ((lane >> 2) & 3);
+    const int pch1 = (2 + half) ^ ((lane >> 2) & 3);
+    bf16x8 a[kLimbs][2];  // a[0] unused: limb 0 lives in a0
+    bf16x8 a0[2][2];      // buffer, half
+    auto lds_a = [&](int t, int li, int ks) {
+        return __builtin_bit_cast(bf16x8, lds.a[t & 3][li][arow][ks ? pch1 : pch0]);
     };
-    auto read_b = [&](OpsB& o, int t, int tn) {
-        o.b[tn] = __builtin_bit_cast(bf16x8, lds.b[t & 1][wn * 4 + tn][lane]);
+    auto read_a = [&](int t, int li, int ks) { a[li][ks] = lds_a(t, li, ks); };
+    auto read_a0 = [&](int buf, int t, int ks) { a0[buf][ks] = lds_a(t, 0, ks); };
+    auto read_b = [&](OpsB& o, int t, int tn, int ks) {
+        o.b[tn][ks] = __builtin_bit_cast(bf16x8, lds.b[t & 1][2 * wn + tn][ks][lane]);
     };
-    auto read_s = [&](OpsB& o, int t, int tn) { o.s[tn] = lds.s[(t >> 2) & 1][wn * 4 + tn][j + 16 * (t & 3)]; };
-    // Window w's MFMA: tile pair p = w / 12 (columns 2p, 2p+1), limb 2 - (w % 12) / 4, then
-    // (tm, tn) = ((w / 2) & 1, 2p + (w & 1)): four independent chains per limb step.
-    auto mfma_w = [&](Sums& r, const OpsA& oa, const OpsB& ob, int w) {
-        const int pr = w / 12, li = 2 - (w % 12) / 4, tm = (w >> 1) & 1, tn = 2 * pr + (w & 1);
-        r.p[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(oa.a[tm][li], ob.b[tn], li == 2 ? zero : r.p[tm][tn], 0,
-                                                              0, 0);
+    const int sw = 4 * wn + ((lane >> 4) & 1);
+    auto read_s = [&](Sums& r, int t, int tn) {
+        r.s[tn] = lds.s[(t >> 2) & 1][sw + 2 * tn][(lane & 15) + 16 * (t & 3)];
     };
-    // Fold operation f (0..71) of the previous group's sums: 8 scale conversions, then per output
-    // a conversion and a float64 FMA: acc += (16 s) * P.
-    float sc16[WN];
-    double scd[WN], pd[2];
+    // Window w's MFMA: limb 2 - w / 4, half (w / 2) & 1, tile w & 1 (two independent chains).
+    auto mfma_w = [&](Sums& r, const OpsB& ob, int abuf, int w) {
+        const int li = 2 - (w >> 2), ks = (w >> 1) & 1, tn = w & 1;
+        const bf16x8 av = li == 0 ? a0[abuf][ks] : a[li][ks];
+        r.p[tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, ob.b[tn][ks], w < 2 ? zero16 : r.p[tn], 0, 0, 0);
+    };
+    // Fold operation f (0..65) of the previous group's sums: the two scales' conversions, then per
+    // tile and result a conversion and a float64 FMA acc += s * P, software-pipelined by one
+    // (conversion of result o + 1 before the FMA of result o).
+    double scd[2], pd[2];
     auto fold_op = [&](const Sums& r, int f) {
-        if (f < 8) {
-            const int tn = f >> 1;
-            if ((f & 1) == 0)
-                sc16[tn] = r.s[tn] * kSixteenthsUnit;
-            else
-                scd[tn] = static_cast<double>(sc16[tn]);
+        if (f < 2) {
+            scd[f] = static_cast<double>(r.s[f]);
+            return;
+        }
+        const int tn = f >= 34 ? 1 : 0;
+        const int e = f - 2 - 32 * tn;  // 0 .. 31
+        if (e == 0) {
+            pd[0] = static_cast<double>(r.p[tn][0]);
+        } else if (e == 31) {
+            acc[tn][15] = fma(scd[tn], pd[1], acc[tn][15]);
+        } else if (e & 1) {
+            const int o = (e + 1) >> 1;  // 1 .. 15
+            pd[o & 1] = static_cast<double>(r.p[tn][o]);
         } else {
-            const int o = (f - 8) >> 1, tn = o >> 3, tm = (o >> 2) & 1, i = o & 3;
-            if ((f & 1) == 0)
-                pd[o & 1] = static_cast<double>(r.p[tm][tn][i]);
-            else
-                acc[tm][tn][i] = fma(scd[tn], pd[o & 1], acc[tm][tn][i]);
+            const int o = (e - 2) >> 1;  // 0 .. 14
+            acc[tn][o] = fma(scd[tn], pd[o & 1], acc[tn][o]);
         }
     };
     auto fold_all = [&](const Sums& r) {
 #pragma unroll
-        for (int f = 0; f < 72; ++f) fold_op(r, f);
+        for (int f = 0; f < 66; ++f) fold_op(r, f);
     };
 
     if (n_groups > 0) {
         // Iteration s computes group s from operand registers read during iteration s - 1 and
-        // folds group s - 1's sums; in its windows it copies stage s + 3, waits for stage s + 1,
-        // decodes its word of it, passes the barrier that publishes it (which also waits for all
-        // of this wavefront's earlier LDS reads, so every buffer copied into has been read by all
-        // wavefronts) and reads stage s + 1's operands.
-        OpsA oa[2];
-        OpsB ob;
+        // folds group s - 1's sums. Window 1 holds the barrier that publishes stage s + 1 (copied
+        // and decoded during iteration s - 1; the barrier also waits for this wavefront's earlier
+        // LDS reads, so once every wavefront passes it stage s's buffers have been read), then
+        // copies stage s + 4 into stage s's buffers. Windows 2 - 8 read stage s + 1's operands,
+        // each register once the MFMAs that use it have issued (limb 2 after window 3, limb 1
+        // after window 7); stage s + 1's scales go straight into the sums slot they will be
+        // folded with, whose scales were converted in window 0. Window 8 waits for stage s + 2's
+        // copies (issued two iterations earlier) and window 11 decodes its word of it.
+        OpsB ob[2];
         Sums sums[2];
 #pragma unroll
-        for (int tn = 0; tn < WN; ++tn) {  // iteration 0 folds these zeros
+        for (int tn = 0; tn < 2; ++tn) {  // iteration 0 folds these zeros
             sums[1].s[tn] = 0.0f;
-#pragma unroll
-            for (int tm = 0; tm < WM; ++tm) sums[1].p[tm][tn] = zero;
+            sums[1].p[tn] = zero16;
         }
         issue(0);
         issue(1);
         issue(2);
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(wide_inflight(1, 2)) : "memory");
-        commit(0);
+        issue(3);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(wide_inflight(1, 3)) : "memory");
+        write_b(0, read_raw(0));
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(wide_inflight(2, 2)) : "memory");
+        write_b(1, read_raw(1));
         barrier();
 #pragma unroll
-        for (int tm = 0; tm < WM; ++tm)
+        for (int li = 1; li < kLimbs; ++li) {
+            read_a(0, li, 0);
+            read_a(0, li, 1);
+        }
+        read_a0(0, 0, 0);
+        read_a0(0, 0, 1);
 #pragma unroll
-            for (int li = 0; li < kLimbs; ++li) read_a(oa[0], 0, tm, li);
-#pragma unroll
-        for (int tn = 0; tn < WN; ++tn) {
-            read_b(ob, 0, tn);
-            read_s(ob, 0, tn);
+        for (int tn = 0; tn < 2; ++tn) {
+            read_b(ob[0], 0, tn, 0);
+            read_b(ob[0], 0, tn, 1);
+            read_s(sums[0], 0, tn);
         }
         for (int s0 = 0; s0 < n_groups; s0 += 4) {
             static_for<4>([&](auto uc) {
                 constexpr int u = decltype(uc)::value;
                 const int s = s0 + u;
                 if (s < n_groups) {  // uniform across the workgroup
-                    OpsA& ca = oa[u & 1];
-                    OpsA& na = oa[(u + 1) & 1];
+                    const OpsB& cb = ob[u & 1];
+                    OpsB& nb = ob[(u + 1) & 1];
                     Sums& cur = sums[u & 1];
-                    const Sums& old = sums[(u + 1) & 1];
+                    Sums& old = sums[(u + 1) & 1];
                     uint32_t raw = 0;
-                    static_for<24>([&](auto wc) {
+                    static_for<12>([&](auto wc) {
                         constexpr int w = decltype(wc)::value;
-                        mfma_w(cur, ca, ob, w);
-                        fold_op(old, 3 * w);
-                        fold_op(old, 3 * w + 1);
-                        fold_op(old, 3 * w + 2);
-                        if constexpr (w == 0) {
-#pragma unroll
-                            for (int tn = 0; tn < WN; ++tn) cur.s[tn] = ob.s[tn];
+                        constexpr int f0 = w < 6 ? 6 * w : 36 + 5 * (w - 6);
+                        constexpr int f1 = w < 6 ? f0 + 6 : f0 + 5;
+                        mfma_w(cur, cb, u & 1, w);
+                        static_for<f1 - f0>([&](auto fc) { fold_op(old, f0 + decltype(fc)::value); });
+                        if constexpr (w == 1) {
+                            barrier();
+                            issue(s + 4);
                         }
-                        if constexpr (w == 1) issue(s + 3);
-                        if constexpr (w == 7) {
-                            // stage s + 1's copies are done once only those of stages s + 2, s + 3 are in flight
-                            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(wide_inflight(u + 2, 2)) : "memory");
-                            raw = reinterpret_cast<const uint32_t*>(
-                                &lds.braw[((s + 1) >> 2) & 1][wid][j + 16 * ((s + 1) & 3)])[q];
+                        if constexpr (w == 2) {
+                            read_b(nb, s + 1, 0, 0);
+                            read_b(nb, s + 1, 0, 1);
                         }
-                        if constexpr (w == 9) lds.b[(s + 1) & 1][wid][lane] = nibbles_bf16_16th(raw);
-                        if constexpr (w == 11) barrier();
-                        if constexpr (w >= 12 && w < 18) read_a(na, s + 1, (w - 12) / 3, (w - 12) % 3);
-                        if constexpr (w == 12 || w == 13) read_b(ob, s + 1, w - 12);
-                        if constexpr (w >= 14 && w < 18) read_s(ob, s + 1, w - 14);
-                        if constexpr (w == 23) {
-                            read_b(ob, s + 1, 2);
-                            read_b(ob, s + 1, 3);
+                        if constexpr (w == 3) {
+                            read_b(nb, s + 1, 1, 0);
+                            read_b(nb, s + 1, 1, 1);
+                            read_s(old, s + 1, 0);
+                            read_s(old, s + 1, 1);
                         }
+                        if constexpr (w == 4) {
+                            read_a(s + 1, 2, 0);
+                            read_a(s + 1, 2, 1);
+                        }
+                        if constexpr (w == 5) {
+                            read_a0((u + 1) & 1, s + 1, 0);
+                            read_a0((u + 1) & 1, s + 1, 1);
+                        }
+                        if constexpr (w == 8) {
+                            read_a(s + 1, 1, 0);
+                            read_a(s + 1, 1, 1);
+                            // stage s + 2's copies are done once only those of stages s + 3, s + 4 are in flight
+                            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(wide_inflight(u + 3, 2)) : "memory");
+                            raw = read_raw(s + 2);
+                        }
+                        if constexpr (w == 11) write_b(s + 2, raw);
                         __builtin_amdgcn_sched_barrier(0);
                     });
                 }
@@ -561,8 +606,9 @@ __global__ __launch_bounds__(512) void q4_gemm_wide_kernel(const uint16_t* xs, c
     }
 
     if (lb != nullptr && blockIdx.y == 0) {
-        // LoRA term on the MFMA (r in the K slot). The stage buffers are free now: the tile's 128
-        // rows of T (its partials summed) and 128 columns of lb are loaded there by the whole
+        // LoRA term on the fp32 MFMA (r in the K slot), added as (lscale / 16) * P since the sums
+        // are multiplied by 16 at the store. The stage buffers are free now: the tile's 128 rows
+        // of T (its partials summed) and 128 columns of lb are loaded there by the whole
         // workgroup at once, rows padded to R + 1 floats, then read as MFMA operands.
         static_assert(sizeof(lds.a) >= sizeof(float) * (128 * (kMaxLoraRank + 1) + kMaxLoraRank * 128),
                       "the LoRA tiles fit in the stage buffers");
@@ -576,37 +622,30 @@ __global__ __launch_bounds__(512) void q4_gemm_wide_kernel(const uint16_t* xs, c
             bs[e] = lb[static_cast<size_t>(e >> 7) * N + min(nt0 + (e & 127), N - 1)];
         }
         __syncthreads();
+        const double s = static_cast<double>(lscale) * 0.0625;
 #pragma unroll
-        for (int tm = 0; tm < WM; ++tm) {
-            const int row_t = wm * 32 + 16 * tm + j;
-#pragma unroll
-            for (int tn = 0; tn < WN; ++tn) {
-                const int col_t = wn * 64 + 16 * tn + j;
-                f32x4 P = zero;
-                for (int r0 = 0; r0 < R; r0 += 4) {
-                    const int r = r0 + q;
-                    const float av = r < R ? ts[row_t * RP + r] : 0.0f;
-                    const float bv = r < R ? bs[r * 128 + col_t] : 0.0f;
-                    P = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, P, 0, 0, 0);
-                }
-                const double s = static_cast<double>(lscale);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[tm][tn][i] = fma(s, static_cast<double>(P[i]), acc[tm][tn][i]);
+        for (int tn = 0; tn < 2; ++tn) {
+            const int col_t = wn * 64 + 32 * tn + col32;
+            f32x16 P = zero16;
+            for (int r0 = 0; r0 < R; r0 += 2) {
+                const int r = r0 + half;
+                const float av = r < R ? ts[arow * RP + r] : 0.0f;
+                const float bv = r < R ? bs[r * 128 + col_t] : 0.0f;
+                P = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, P, 0, 0, 0);
             }
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[tn][v] = fma(s, static_cast<double>(P[v]), acc[tn][v]);
         }
     }
 
     float* dst = out + static_cast<size_t>(blockIdx.y) * M * N;
 #pragma unroll
-    for (int tm = 0; tm < WM; ++tm) {
+    for (int tn = 0; tn < 2; ++tn) {
+        const int col = n0 + 32 * tn + col32;
 #pragma unroll
-        for (int tn = 0; tn < WN; ++tn) {
-            const int col = n0 + 16 * tn + j;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int row = m0 + 16 * tm + 4 * q + i;
-                if (row < M && col < N) dst[static_cast<size_t>(row) * N + col] = static_cast<float>(acc[tm][tn][i]);
-            }
+        for (int v = 0; v < 16; ++v) {
+            const int row = m0 + 8 * (v >> 2) + 4 * half + (v & 3);
+            if (row < M && col < N) dst[static_cast<size_t>(row) * N + col] = static_cast<float>(acc[tn][v] * 16.0);
         }
     }
 }

@@ -1,7 +1,8 @@
 """Arithmetic facts behind the bf16-limb MFMA paths, checked on the CPU.
 
-The wide int4 GEMM and the CQ4 MFMA GEMM feed v_mfma_f32_16x16x32_bf16 with x split into three
-bf16 limbs (split_bf16_limbs in q4_device.hpp: b0 = x truncated to its top 8 significant bits,
+The wide int4 GEMM (v_mfma_f32_32x32x16_bf16) and the CQ4 MFMA GEMM (v_mfma_f32_16x16x32_bf16) feed
+the matrix cores with x split into three bf16 limbs (split_bf16_limbs in q4_device.hpp: b0 = x
+truncated to its top 8 significant bits,
 b1 = (x - b0) truncated the same way, b2 = x - b0 - b1) and, for CQ4, each fp16 codebook value split
 into two limbs (top 8 significant bits and the rest). The kernels' products are exact when
   - b0 + b1 + b2 == x (both subtractions exact, b2 representable in bf16), which holds for every
