@@ -247,25 +247,33 @@ __device__ __forceinline__ void static_for(F&& f) {
 // Limbs per x value on the bf16 MFMA path.
 constexpr int kLimbs = 3;
 
-// x (fp32, M x K) -> x limbs (bf16, [M][KB][3][64] with KB = ceil(K / 64), rows
-// zero-padded to KB * 64 values) for q4_gemm_wide_kernel. Each value is split by
-// split_bf16_limbs (b0 + b1 + b2 == x for |x| >= 2^-110, within 2^-133 below), and a
-// product of a limb with a bf16 weight v/16 is exact in fp32.
-// One thread per 8 consecutive values of a row: two 16-byte loads, three
-// 16-byte stores (one per limb), coalesced along the row.
+// x (fp32, M x K) -> x limbs (bf16) for q4_gemm_wide_kernel, laid out the way its copies
+// consume them: [ceil(M/16)][K/32][3][16][4][8] = (16-row block, group, limb, row of the block,
+// 16-byte slot, value). Slot s of row r holds the row's values 8c .. 8c+7 of the group with
+// c = s ^ ((r >> 2) & 3), the kernel's LDS chunk swizzle, so a wavefront copies one limb of one
+// group of a 16-row block as one contiguous 1 KiB run (8 full cache lines). Rows >= M are zero.
+// Each value is split by split_bf16_limbs (b0 + b1 + b2 == x for |x| >= 2^-110, within 2^-133
+// below), and a product of a limb with a bf16 weight v/16 is exact in fp32.
+// One thread per (block, group, row, slot): two 16-byte loads (4 threads read one row's 128
+// bytes of the group), three 16-byte stores, each store instruction of a wavefront one 1 KiB run.
+constexpr int kLimbBlockValues = 16 * 32;  // one limb of one group of a 16-row block (1 KiB)
+
 __device__ __forceinline__ void split_x_block(const float* __restrict__ x, uint16_t* __restrict__ xs, int M, int K,
-                                              int KB, int block) {
+                                              int block) {
+    const int G = K >> 5;
     const size_t idx = static_cast<size_t>(block) * 256 + threadIdx.x;
-    const size_t per_row = static_cast<size_t>(KB) * 8;
-    if (idx >= static_cast<size_t>(M) * per_row) return;
-    const int row = static_cast<int>(idx / per_row);
-    const int c8 = static_cast<int>(idx % per_row);
-    const int kb = c8 >> 3, c = c8 & 7;
-    const int k0 = kb * 64 + c * 8;
+    const size_t unit = idx >> 6;  // (16-row block, group)
+    if (unit >= static_cast<size_t>((M + 15) >> 4) * G) return;
+    const int lane = static_cast<int>(idx & 63);
+    const int rr = lane >> 2;
+    const int c = (lane & 3) ^ ((rr >> 2) & 3);
+    const int row = static_cast<int>(unit / G) * 16 + rr;
+    const int g = static_cast<int>(unit % G);
     float v[8];
-    if (k0 < K) {  // K % 32 == 0, so the 8 values are all inside the row or all past it
-        const f32x4 lo = *reinterpret_cast<const f32x4*>(x + static_cast<size_t>(row) * K + k0);
-        const f32x4 hi = *reinterpret_cast<const f32x4*>(x + static_cast<size_t>(row) * K + k0 + 4);
+    if (row < M) {
+        const float* src = x + static_cast<size_t>(row) * K + g * 32 + c * 8;
+        const f32x4 lo = *reinterpret_cast<const f32x4*>(src);
+        const f32x4 hi = *reinterpret_cast<const f32x4*>(src + 4);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             v[t] = lo[t];
@@ -284,14 +292,9 @@ __device__ __forceinline__ void split_x_block(const float* __restrict__ x, uint1
 #pragma unroll
         for (int li = 0; li < kLimbs; ++li) limb[li][t] = lo[li] | (hi[li] << 16);
     }
-    uint16_t* dst = xs + (static_cast<size_t>(row) * KB + kb) * (kLimbs * 64) + c * 8;
+    uint16_t* dst = xs + unit * (kLimbs * kLimbBlockValues) + lane * 8;
 #pragma unroll
-    for (int li = 0; li < kLimbs; ++li) *reinterpret_cast<u32x4*>(dst + li * 64) = limb[li];
-}
-
-__global__ __launch_bounds__(256) void split_x_kernel(const float* __restrict__ x, uint16_t* __restrict__ xs,
-                                                      int M, int K, int KB) {
-    split_x_block(x, xs, M, K, KB, blockIdx.x);
+    for (int li = 0; li < kLimbs; ++li) *reinterpret_cast<u32x4*>(dst + li * kLimbBlockValues) = limb[li];
 }
 
 // Wide tile for M > 32 (prefill, LoRA projections): 128 x 128 outputs per workgroup of 8
@@ -386,7 +389,6 @@ __global__ __launch_bounds__(512) void q4_gemm_wide_kernel(const uint16_t* xs, c
     const int col32 = lane & 31;
     const int half = lane >> 5;
     const int G = K >> 5;
-    const int KB = (G + 1) >> 1;
 
     int tile_m, tile_n;
     wide_tile(tiles_m, tiles_n, tile_m, tile_n);
@@ -397,11 +399,15 @@ __global__ __launch_bounds__(512) void q4_gemm_wide_kernel(const uint16_t* xs, c
     const int g_end = min(G, g_begin + groups_per_split);
     const int n_groups = g_end - g_begin;
 
-    // x-limb copy of this wavefront: rows 16 wid .. 16 wid + 15 of the tile; lane i fills chunk
-    // slot i & 3 of row 16 wid + (i >> 2), which holds logical chunk (i & 3) ^ ((i >> 4) & 3).
-    const uint16_t* asrc =
-        xs + static_cast<size_t>(min(mt0 + 16 * wid + (lane >> 2), M - 1)) * KB * (kLimbs * 64) +
-        8 * ((lane & 3) ^ ((lane >> 4) & 3));
+    // x-limb copy of this wavefront: the 16-row block of tile rows 16 wid .. 16 wid + 15, one
+    // contiguous 1 KiB run per limb (split_x_block lays the rows out swizzled as the LDS reads
+    // expect). Blocks past the last one (rows past M, never stored) re-read the last block. The
+    // address is a uniform base advanced per stage in scalar registers plus lane * 16 bytes, and
+    // each limb's offset is the instruction's immediate (added to both addresses).
+    const int xblocks = (M + 15) >> 4;
+    const char* abase = reinterpret_cast<const char*>(
+        xs + static_cast<size_t>(min((mt0 >> 4) + wid, xblocks - 1)) * G * (kLimbs * kLimbBlockValues));
+    const uint32_t aoff = static_cast<uint32_t>(lane) * 16;
     // Quad copies: tile column 16 wid + (lane & 15), group 4Q + (lane >> 4) of the quad.
     const int qcol = min(nt0 + 16 * wid + (lane & 15), N - 1);
     const u32x4* bsrc = reinterpret_cast<const u32x4*>(wq + static_cast<size_t>(qcol) * (K >> 3));
@@ -411,10 +417,13 @@ __global__ __launch_bounds__(512) void q4_gemm_wide_kernel(const uint16_t* xs, c
     // Copies of stage t of this split (clamped into it).
     auto issue = [&](int t) {
         const int g = g_begin + min(t, n_groups - 1);
-        const uint16_t* src = asrc + static_cast<size_t>(g >> 1) * (kLimbs * 64) + 32 * (g & 1);
-#pragma unroll
-        for (int li = 0; li < kLimbs; ++li)
-            __builtin_amdgcn_global_load_lds(src + li * 64, &lds.a[t % kWideStages][li][16 * wid][0], 16, 0, 0);
+        const char* src = abase + static_cast<size_t>(g) * (kLimbs * kLimbBlockValues * sizeof(uint16_t));
+        static_for<kLimbs>([&](auto lc) {
+            constexpr int li = decltype(lc)::value;
+            constexpr int kLimbBytes = kLimbBlockValues * sizeof(uint16_t);
+            char* dst = reinterpret_cast<char*>(&lds.a[t % kWideStages][li][16 * wid][0]) - li * kLimbBytes;
+            __builtin_amdgcn_global_load_lds(src + aoff, dst, 16, li * kLimbBytes, 0);
+        });
         if (t % 4 == 0) {  // uniform
             const int gq = g_begin + min(t + qg, n_groups - 1);
             const int qb = (t >> 2) & 1;
@@ -480,9 +489,11 @@ __global__ __launch_bounds__(512) void q4_gemm_wide_kernel(const uint16_t* xs, c
         r.p[tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, ob.b[tn][ks], w < 2 ? zero16 : r.p[tn], 0, 0, 0);
     };
     // Fold operation f (0..65) of the previous group's sums: the two scales' conversions, then per
-    // tile and result a conversion and a float64 FMA acc += s * P, software-pipelined by one
-    // (conversion of result o + 1 before the FMA of result o).
-    double scd[2], pd[2];
+    // tile and result a conversion and a float64 FMA acc += s * P, software-pipelined by
+    // kFoldDepth (the conversion of result o + kFoldDepth issues right after the FMA of result o,
+    // so each FMA's operand was converted kFoldDepth - 1 operations earlier).
+    constexpr int kFoldDepth = 4;
+    double scd[2], pd[kFoldDepth];
     auto fold_op = [&](const Sums& r, int f) {
         if (f < 2) {
             scd[f] = static_cast<double>(r.s[f]);
@@ -490,16 +501,18 @@ __global__ __launch_bounds__(512) void q4_gemm_wide_kernel(const uint16_t* xs, c
         }
         const int tn = f >= 34 ? 1 : 0;
         const int e = f - 2 - 32 * tn;  // 0 .. 31
-        if (e == 0) {
-            pd[0] = static_cast<double>(r.p[tn][0]);
-        } else if (e == 31) {
-            acc[tn][15] = fma(scd[tn], pd[1], acc[tn][15]);
-        } else if (e & 1) {
-            const int o = (e + 1) >> 1;  // 1 .. 15
-            pd[o & 1] = static_cast<double>(r.p[tn][o]);
+        auto cvt = [&](int o) { pd[o % kFoldDepth] = static_cast<double>(r.p[tn][o]); };
+        auto fold = [&](int o) { acc[tn][o] = fma(scd[tn], pd[o % kFoldDepth], acc[tn][o]); };
+        if (e < kFoldDepth) {
+            cvt(e);
+        } else if (e < 32 - kFoldDepth) {
+            const int k = e - kFoldDepth;
+            if (k & 1)
+                cvt(kFoldDepth + (k >> 1));
+            else
+                fold(k >> 1);
         } else {
-            const int o = (e - 2) >> 1;  // 0 .. 14
-            acc[tn][o] = fma(scd[tn], pd[o & 1], acc[tn][o]);
+            fold(e - 16);
         }
     };
     auto fold_all = [&](const Sums& r) {
@@ -720,11 +733,11 @@ __device__ __forceinline__ void lora_t_block(const float* __restrict__ x, const 
 // come first because each runs a long dependent chain (all of its loads, then its MFMAs): started
 // last, behind the many short split workgroups, they set the launch's end.
 __global__ __launch_bounds__(256) void prep_kernel(const float* __restrict__ x, uint16_t* __restrict__ xs, int M,
-                                                   int K, int KB, int lora_blocks, const float* __restrict__ la,
+                                                   int K, int lora_blocks, const float* __restrict__ la,
                                                    float* __restrict__ tpart, int R, int tiles_m_t, int tiles_r) {
     const int b = static_cast<int>(blockIdx.x);
     if (b >= lora_blocks) {
-        split_x_block(x, xs, M, K, KB, b - lora_blocks);
+        split_x_block(x, xs, M, K, b - lora_blocks);
         return;
     }
     lora_t_block(x, la, tpart, M, K, R, b % tiles_m_t, (b / tiles_m_t) % tiles_r, b / (tiles_m_t * tiles_r));
@@ -973,15 +986,7 @@ size_t align_up(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 }  // namespace
 
 size_t split_x_bf16_bytes(uint32_t m, uint32_t k) {
-    return static_cast<size_t>(m) * ((k / kGroup + 1) / 2) * kLimbs * 64 * sizeof(uint16_t);
-}
-
-hipError_t launch_split_x_bf16(const float* x, uint16_t* xs, uint32_t m, uint32_t k, hipStream_t stream) {
-    const int KB = static_cast<int>((k / kGroup + 1) / 2);
-    const size_t chunks = static_cast<size_t>(m) * KB * 8;
-    hipLaunchKernelGGL(split_x_kernel, dim3(static_cast<unsigned>((chunks + 255) / 256)), dim3(256), 0, stream, x, xs,
-                       static_cast<int>(m), static_cast<int>(k), KB);
-    return hipGetLastError();
+    return static_cast<size_t>((m + 15) / 16) * 16 * k * kLimbs * sizeof(uint16_t);
 }
 
 Q4Plan plan_q4gemm(const DeviceInfo& dev, uint32_t m, uint32_t n, uint32_t k, uint32_t rank) {
@@ -1053,13 +1058,13 @@ hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float*
     // One preparation launch: the bf16 limbs of x for the wide kernel and/or the LoRA T partials.
     uint16_t* xs = plan.kind == Q4Plan::kWide ? reinterpret_cast<uint16_t*>(wsp) : nullptr;
     {
-        const int KB = static_cast<int>((k / kGroup + 1) / 2);
-        const int split_blocks = xs ? static_cast<int>((static_cast<size_t>(m) * KB * 8 + 255) / 256) : 0;
+        // split_x_block: 64 threads per (16-row block, group)
+        const int split_blocks = xs ? static_cast<int>(((m + 15) / 16 * static_cast<size_t>(k / kGroup) * 64 + 255) / 256) : 0;
         const int tiles_m_t = static_cast<int>((m + 15) / 16), tiles_r = static_cast<int>((rank + 15) / 16);
         const int lora_blocks = rank ? tiles_m_t * tiles_r * plan.t_splits : 0;
         if (split_blocks + lora_blocks > 0) {
             hipLaunchKernelGGL(prep_kernel, dim3(static_cast<unsigned>(split_blocks + lora_blocks)), dim3(256), 0,
-                               stream, x, xs, mm, kk, KB, lora_blocks, la, tpart, rr, tiles_m_t, tiles_r);
+                               stream, x, xs, mm, kk, lora_blocks, la, tpart, rr, tiles_m_t, tiles_r);
             const hipError_t pe = hipGetLastError();
             if (pe != hipSuccess) return pe;
         }

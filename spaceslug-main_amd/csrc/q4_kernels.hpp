@@ -49,11 +49,10 @@ hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float*
                          uint32_t n, uint32_t k, const float* la, const float* lb, uint32_t rank,
                          float lora_scale, void* workspace, hipStream_t stream);
 
-// x (fp32, m x k, k % 32 == 0) -> three exact bf16 limbs per value, laid out [m][ceil(k/64)][3][64]
-// (rows zero-padded to a multiple of 64 values); split_x_bf16_bytes(m, k) bytes at xs. The wide
-// int4 GEMM reads this layout (the CQ4 transform writes the same layout for its MFMA GEMM).
+// Bytes of the wide int4 GEMM's x limbs for x (fp32, m x k, k % 32 == 0): three exact bf16 limbs
+// per value in 16-row blocks (rows padded with zeros to a multiple of 16), written by the
+// preparation launch of launch_q4gemm and part of plan.workspace_bytes.
 size_t split_x_bf16_bytes(uint32_t m, uint32_t k);
-hipError_t launch_split_x_bf16(const float* x, uint16_t* xs, uint32_t m, uint32_t k, hipStream_t stream);
 
 // fp32 w[k][n] (row-major) -> packed int4 weights [n][k/2] and scales [n][k/32]; k % 32 == 0 and
 // k / 32 <= 65535 (checked by the caller). Rule at q4_quantize.hip.
