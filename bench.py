@@ -448,7 +448,7 @@ def gemv_ceiling(torch, steps: int, m: int, n: int, k: int, bytes_per_launch: in
     fills = [torch.empty(1, dtype=torch.float32, device="cuda") for _ in range(64)]
     fill_us = _graph_per_launch_us(torch, lambda i: fills[i].fill_(1.0), 64, iters)
     reads = {}
-    for rb, unroll in ((512, 4), (512, 8), (1024, 4), (1024, 8), (2048, 8)):
+    for rb, unroll in ((192, 16), (256, 16), (512, 8), (512, 16), (1024, 8)):
         t = time_each(torch, lambda: check(lib.spaceslug_probe_read(vp(buf.data_ptr()), total, vp(ybuf.data_ptr()),
                                                                      rb, unroll, stream())), MIN_TIMED, 2)
         reads[f"{rb}x256 threads, {unroll} loads in flight"] = round(total / (t["median"] * 1e-3) / 1e9, 1)
