@@ -16,6 +16,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 #include <utility>
 
 #include "cq4_kernels.hpp"
@@ -39,6 +40,16 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t h) { return static_
 
 __device__ __forceinline__ uint16_t float_to_half_bits(float f) {
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));  // round to nearest even
+}
+
+// fp16 bits of a double, rounded to nearest even. Rounding to float first and then to fp16 gives the
+// same result (24 >= 2 * 11 + 2 significant bits, so the first rounding cannot create a tie for the
+// second); the empty asm keeps the compiler from fusing the two hardware conversions (v_cvt_f32_f64,
+// v_cvt_f16_f32) into one from double, which it expands into about 40 integer instructions.
+__device__ __forceinline__ uint16_t double_to_half_bits(double d) {
+    float f = static_cast<float>(d);
+    asm("" : "+v"(f));
+    return float_to_half_bits(f);
 }
 
 // Per-element input scale reciprocal (cactus_x86.cpp:74-80).
@@ -283,7 +294,7 @@ __global__ __launch_bounds__(256) void cq4_gemm_kernel(Cq4View w, const float* _
     }
 #pragma unroll
     for (int r = 0; r < ROWS; ++r)
-        if (m0 + r < M) c[static_cast<size_t>(m0 + r) * w.N + n] = float_to_half_bits(static_cast<float>(acc[r]));
+        if (m0 + r < M) c[static_cast<size_t>(m0 + r) * w.N + n] = double_to_half_bits(acc[r]);
 }
 
 // Up to 4 rows with 4-bit indices in either layout and word-aligned groups
@@ -349,7 +360,7 @@ __global__ __launch_bounds__(256) void cq4_gemv_kernel(Cq4View w, const float* _
     if (lane == 0)
 #pragma unroll
         for (int r = 0; r < ROWS; ++r)
-            if (static_cast<uint32_t>(r) < M) c[static_cast<size_t>(r) * w.N + n] = float_to_half_bits(static_cast<float>(acc[r]));
+            if (static_cast<uint32_t>(r) < M) c[static_cast<size_t>(r) * w.N + n] = double_to_half_bits(acc[r]);
 }
 
 // MFMA form for 4-bit LSB-packed indices (the packing of cactus_x86.cpp:24-43 with
@@ -544,52 +555,60 @@ __global__ __launch_bounds__(256) void cq4_gemm_mfma_kernel(Cq4View w, const uin
             for (int i = 0; i < 4; ++i) {
                 const int row = m0 + 16 * tm + 4 * q + i;
                 if (row < Mi && col < N)
-                    c[static_cast<size_t>(row) * N + col] = float_to_half_bits(static_cast<float>(acc[tm][tn][i]));
+                    c[static_cast<size_t>(row) * N + col] = double_to_half_bits(acc[tm][tn][i]);
             }
         }
 }
 
-// The same 64 x 64 tiles, operand layouts, MFMA chains and float64 fold as
-// cq4_gemm_mfma_kernel, with a deeper copy pipeline and twice the wavefronts; taken when
-// the tile's norms fit in LDS (ng <= 128, i.e. K <= 4096 at group size 32). The kernel
-// above runs one wavefront per SIMD with one 64-value stage in flight, so every LDS read,
-// copy and MFMA dependency is exposed (1024^3: ~1.7 us per stage against ~0.3 us of
-// matrix-core work). Here:
-//   - 8 wavefronts, two per SIMD: wavefront w owns rows 16 (w % 4) .. +15 and columns
-//     32 (w / 4) .. +31 of the tile (1 x 2 MFMA tiles), so one wavefront's LDS waits and
-//     VALU work (decode, fold) run while the other's MFMAs issue;
-//   - every operand reaches LDS by global_load_lds, kCq4Stages stages deep: the
-//     activation limbs (wavefront w copies the 8-row block w of each limb, three 1 KiB
-//     copies) and the packed indices as copied (4 bytes per thread: the word this thread
-//     decodes, so a thread waits only for its own wavefront's copies), decoded one stage
-//     ahead into a double-buffered MFMA B layout; the norms of the tile's 64 columns, all
-//     groups, are read once before the loop;
-//   - iteration t copies stage t + 3 into slot (t + 3) % 4, which no live stage holds
-//     (past the last stage the copied stage is clamped, so every wavefront issues the same
-//     4 copies per stage and `s_waitcnt vmcnt(8)` leaves exactly the two younger stages in
-//     flight), reads stage t's operands, waits for stage t + 1, decodes it, runs stage t's
-//     MFMAs and folds, and passes one barrier. The loop issues no other vector-memory
+// Pipelined MFMA GEMM for 4-bit LSB-packed indices, taken when the tile's norms fit in LDS
+// (ng <= 128, i.e. K <= 4096 at group size 32). The same 64 x 64 tiles, activation-limb
+// layout, codebook limbs and float64 fold as cq4_gemm_mfma_kernel above, on
+// v_mfma_f32_32x32x16_bf16 (32 matrix-core cycles) with a deeper copy pipeline:
+//   - 8 wavefronts, two per SIMD: wavefront w owns the 32 x 32 output tile (rows 32 (w & 1),
+//     columns 32 ((w >> 1) & 1)) for the sub-group (w >> 2) of every 64-value stage, so the
+//     two wavefronts of a SIMD (w, w + 4) share a tile and split K between them. Per stage a
+//     wavefront runs one chain of 12 MFMAs (3 activation limbs x 2 codebook limbs x 2 halves of
+//     16 values, smallest products first; dependent 32x32x16 MFMAs issue back to back), and the
+//     two halves of K are added in double at the end, through LDS, before the fp16 rounding.
+//     On gfx950 a 32x32x16 MFMA leaves room for about 6 VALU instructions in the issue pipe it
+//     shares with them (a 16x16x32 for about 2), so the previous stage's fold (16 conversions
+//     and 16 float64 FMAs per wavefront) is laid between the chain's MFMAs;
+//   - lane l of a 32x32x16 MFMA holds A[row l % 32][k = 8 (l / 32) .. +7] and B[k = 8 (l / 32)
+//     .. +7][column l % 32], and result element v is row 8 (v / 4) + 4 (l / 32) + v % 4 of
+//     column l % 32 (one column per lane, one norm per stage);
+//   - every operand reaches LDS by global_load_lds, kCq4Stages stages deep: the activation limbs
+//     (wavefront w copies the 8-row block w of each limb, three 1 KiB copies) and the packed
+//     indices as copied (4 bytes per thread: the word this thread decodes, so a thread waits only
+//     for its own wavefront's copies), decoded one stage ahead into a double-buffered MFMA B layout
+//     (sub-group, codebook limb, 32-column tile, half, slot); the norms of the tile's 64 columns,
+//     all groups, are read once before the loop;
+//   - iteration t copies stage t + 3 into slot (t + 3) % 4, which no live stage holds (past the
+//     last stage the copied stage is clamped, so every wavefront issues the same 4 copies per
+//     stage and `s_waitcnt vmcnt(8)` leaves exactly the two younger stages in flight), reads stage
+//     t's operands, waits for stage t + 1, decodes it, runs stage t's MFMAs with stage t - 1's
+//     fold between them, and passes one barrier. The loop issues no other vector-memory
 //     instruction.
 constexpr int kCq4Stages = 4;
 constexpr int kCq4PipeWaves = 8;
 constexpr uint32_t kCq4NormsMax = 128;  // norm groups per column held in LDS
 
 struct Cq4PipeLds {
-    u32x4 a[kCq4Stages][kCq4Limbs][8][64];  // as Cq4MfmaStage::a, per stage
-    uint32_t braw[kCq4Stages][512];         // stage, thread: its packed word as copied
-    u32x4 b[2][2][2][4][64];                // stage parity, sub-group, codebook limb, 16-column tile, slot
-    uint16_t norms[kCq4NormsMax][kCq4Tile]; // group, tile column (fp16 bits)
+    u32x4 a[kCq4Stages][kCq4Limbs][8][64];   // as Cq4MfmaStage::a, per stage
+    uint32_t braw[kCq4Stages][512];          // stage, thread: its packed word as copied
+    u32x4 b[2][2][2][2][2][64];              // stage parity, sub-group, codebook limb, 32-column tile, half, slot
+    uint16_t norms[kCq4NormsMax][kCq4Tile];  // group, tile column (fp16 bits)
     uint32_t lut[16];
 };
 static_assert(sizeof(Cq4PipeLds) <= 160 * 1024, "LDS budget");
 
-// Slot of the decoded B entry for column j and word q within its 64-slot tile: 16 q + (j xor m(q)),
-// m = 0, 12, 4, 8. gfx950 serves 128-bit LDS accesses 16 lanes per cycle (in a half-wavefront, the
-// 4-lane chunks whose index has even parity together, then the odd ones), and two of those lanes
-// conflict when their addresses agree modulo 256 bytes. A decoding thread's 4-lane chunk holds one
-// column's 4 words and a cycle 4 columns, an MFMA reader's cycle 8 columns of two words: with
-// these masks both see 16 distinct 16-byte bank groups (plain j + 16 q conflicts 4-way on the writes).
-__device__ __forceinline__ int cq4_b_slot(int j, int q) { return 16 * q + (j ^ ((0x84C0 >> (4 * q)) & 0xF)); }
+// Address of the B operand of lane slot s (column s % 32, word 2 half + s / 32 of the sub-group)
+// of half `half`: s ^ 4 ((s >> 5) & 1) ^ 8 half. gfx950 serves 128-bit LDS reads 16 lanes per cycle
+// (in a half-wavefront, the 4-lane chunks whose index has even popcount parity together, then the
+// odd ones) and 128-bit writes 16 consecutive lanes per cycle; two lanes of a cycle conflict when
+// their addresses agree modulo 256 bytes. With this map the MFMA operand reads (lane l reads slot l
+// of one half) and the decode writes (thread 4 c + w writes column c's word w to half w / 2, slot
+// c + 32 (w % 2)) both touch 16 distinct 16-byte bank groups per cycle.
+__device__ __forceinline__ int cq4_b_addr(int s, int half) { return s ^ (4 * ((s >> 5) & 1)) ^ (8 * half); }
 
 __global__ __launch_bounds__(64 * kCq4PipeWaves) void cq4_gemm_pipe_kernel(Cq4View w, const uint16_t* __restrict__ xs,
                                                                           uint16_t* __restrict__ c, uint32_t M,
@@ -598,15 +617,14 @@ __global__ __launch_bounds__(64 * kCq4PipeWaves) void cq4_gemm_pipe_kernel(Cq4Vi
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wid & 3, wn = wid >> 2;
-    const int j = lane & 15, q = lane >> 4;
+    const int wm = wid & 1, wn = (wid >> 1) & 1, ku = wid >> 2;
+    const int col32 = lane & 31, half = lane >> 5;
     const int K = static_cast<int>(w.K), N = static_cast<int>(w.N), Mi = static_cast<int>(M);
     const int T = K / 64;
     const int spg = static_cast<int>(gs) >> 5;
     const int G = static_cast<int>(ng);
     const int mt0 = static_cast<int>(blockIdx.x % tiles_m) * kCq4Tile;
     const int nt0 = static_cast<int>(blockIdx.x / tiles_m) * kCq4Tile;
-    const int m0 = mt0 + 16 * wm, n0 = nt0 + 32 * wn;
 
     // Activation-limb copy of this wavefront: 8-row block wid (row pairs 4 wid .. 4 wid + 3).
     const uint16_t* asrc;
@@ -619,10 +637,14 @@ __global__ __launch_bounds__(64 * kCq4PipeWaves) void cq4_gemm_pipe_kernel(Cq4Vi
     const int bu = tid >> 8, bc = (tid >> 2) & 63, bw = tid & 3;
     const uint32_t* bsrc =
         reinterpret_cast<const uint32_t*>(w.packed + static_cast<size_t>(min(nt0 + bc, N - 1)) * (K >> 1)) + bw;
-    const int blane = cq4_b_slot(bc & 15, bw);
-    const int bslot = cq4_b_slot(j, q);
-    const int pr = (16 * wm + j) >> 1;  // this lane's A row pair
-    const int arow = pr * 16 + 8 * (j & 1);
+    const int bdst = cq4_b_addr((bc & 31) + 32 * (bw & 1), bw >> 1);
+    // This lane's A operand: row 32 wm + (lane & 31), chunk 4 ku + 2 h + (lane >> 5) of a stage for
+    // half h (the layout of Cq4MfmaStage::a).
+    const int ar = 32 * wm + col32;
+    const int apr = ar >> 1;
+    const int aidx0 = apr * 16 + 8 * (ar & 1) + ((4 * ku + half) ^ (apr & 7));
+    const int aidx1 = apr * 16 + 8 * (ar & 1) + ((4 * ku + 2 + half) ^ (apr & 7));
+    const int bsrc0 = cq4_b_addr(lane, 0), bsrc1 = cq4_b_addr(lane, 1);
 
     // Stage t's copies into stage slot st (past the last stage, t is clamped and st is not).
     auto issue = [&](int t, int st) {
@@ -644,8 +666,8 @@ __global__ __launch_bounds__(64 * kCq4PipeWaves) void cq4_gemm_pipe_kernel(Cq4Vi
             hi[i] = __builtin_amdgcn_perm(e[2 * i + 1], e[2 * i], 0x05040100u);  // low halves
             lo[i] = __builtin_amdgcn_perm(e[2 * i + 1], e[2 * i], 0x07060302u);  // high halves
         }
-        lds.b[par][bu][0][bc >> 4][blane] = hi;
-        lds.b[par][bu][1][bc >> 4][blane] = lo;
+        lds.b[par][bu][0][bc >> 5][bw >> 1][bdst] = hi;
+        lds.b[par][bu][1][bc >> 5][bw >> 1][bdst] = lo;
     };
     auto barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
@@ -679,80 +701,114 @@ __global__ __launch_bounds__(64 * kCq4PipeWaves) void cq4_gemm_pipe_kernel(Cq4Vi
     decode(0);
     barrier();
 
-    const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
-    double acc[2][4];
+    f32x16 zero16;
 #pragma unroll
-    for (int tn = 0; tn < 2; ++tn)
+    for (int v = 0; v < 16; ++v) zero16[v] = 0.0f;
+    double acc[16];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[tn][i] = 0.0;
-
-    for (int t = 0; t < T; ++t) {
-        issue(min(t + 3, T - 1), (t + 3) & (kCq4Stages - 1));
-        const int st = t & (kCq4Stages - 1), par = t & 1;
-        bf16x8 bh[2][2], bl[2][2], av[2][kCq4Limbs];
-        double nv[2][2];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-#pragma unroll
-            for (int tn = 0; tn < 2; ++tn) {
-                bh[u][tn] = __builtin_bit_cast(bf16x8, lds.b[par][u][0][wn * 2 + tn][bslot]);
-                bl[u][tn] = __builtin_bit_cast(bf16x8, lds.b[par][u][1][wn * 2 + tn][bslot]);
-            }
-            const int idx = arow + ((4 * u + q) ^ (pr & 7));
-#pragma unroll
-            for (int li = 0; li < kCq4Limbs; ++li) av[u][li] = __builtin_bit_cast(bf16x8, (&lds.a[st][li][0][0])[idx]);
-            const int g = (2 * t + u) / spg;
-#pragma unroll
-            for (int tn = 0; tn < 2; ++tn)
-                nv[u][tn] = static_cast<double>(half_bits_to_float(lds.norms[g][32 * wn + 16 * tn + j]));
+    for (int v = 0; v < 16; ++v) acc[v] = 0.0;
+    // Chain step i (0 .. 11): activation limb, codebook limb (0 high, 1 low) and half, the
+    // products smallest first: (2, lo), (1, lo), (2, hi), (0, lo), (1, hi), (0, hi), each over
+    // both halves.
+    struct Stage {
+        f32x16 p;
+        double norm;
+    };
+    Stage st_buf[2];
+    st_buf[1].p = zero16;  // iteration 0 folds these zeros
+    st_buf[1].norm = 0.0;
+    // fold operation f (0 .. 31) of a stage: per result a conversion, then (one result later) a
+    // float64 FMA acc += norm * P
+    double pd[2];
+    auto fold_op = [&](const Stage& r, int f) {
+        if (f == 0) {
+            pd[0] = static_cast<double>(r.p[0]);
+        } else if (f == 31) {
+            acc[15] = fma(r.norm, pd[1], acc[15]);
+        } else if (f & 1) {
+            const int o = (f + 1) >> 1;  // 1 .. 15
+            pd[o & 1] = static_cast<double>(r.p[o]);
+        } else {
+            const int o = (f - 2) >> 1;  // 0 .. 14
+            acc[o] = fma(r.norm, pd[o & 1], acc[o]);
         }
-        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // this wavefront's copies of stage t + 1
-        decode(t + 1);  // past the last stage: rewrites an unread buffer from a clamped copy
-        // Four independent chains (sub-group u, column tile tn), interleaved step by step; each
-        // chain adds its six limb products smallest first.
-        f32x4_t P[2][2];
+    };
+
+    for (int t0 = 0; t0 < T; t0 += 2) {
+        static_for<2>([&](auto uc) {
+            constexpr int u = decltype(uc)::value;
+            const int t = t0 + u;
+            if (t < T) {  // uniform
+                Stage& cur = st_buf[u];
+                const Stage& old = st_buf[u ^ 1];
+                issue(min(t + 3, T - 1), (t + 3) & (kCq4Stages - 1));
+                const int sidx = t & (kCq4Stages - 1), par = t & 1;
+                bf16x8 av[kCq4Limbs][2], bv[2][2];
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+                for (int li = 0; li < kCq4Limbs; ++li) {
+                    av[li][0] = __builtin_bit_cast(bf16x8, (&lds.a[sidx][li][0][0])[aidx0]);
+                    av[li][1] = __builtin_bit_cast(bf16x8, (&lds.a[sidx][li][0][0])[aidx1]);
+                }
 #pragma unroll
-            for (int tn = 0; tn < 2; ++tn) P[u][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[u][2], bl[u][tn], zero, 0, 0, 0);
+                for (int cl = 0; cl < 2; ++cl) {
+                    bv[cl][0] = __builtin_bit_cast(bf16x8, lds.b[par][ku][cl][wn][0][bsrc0]);
+                    bv[cl][1] = __builtin_bit_cast(bf16x8, lds.b[par][ku][cl][wn][1][bsrc1]);
+                }
+                cur.norm = static_cast<double>(half_bits_to_float(lds.norms[(2 * t + ku) / spg][32 * wn + col32]));
+                asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // this wavefront's copies of stage t + 1
+                decode(t + 1);  // past the last stage: rewrites an unread buffer from a clamped copy
+                static_for<12>([&](auto ic) {
+                    constexpr int i = decltype(ic)::value;
+                    constexpr int pr = i >> 1, h = i & 1;
+                    constexpr int li = (0x010212 >> (4 * pr)) & 0xF;  // 2, 1, 2, 0, 1, 0
+                    constexpr int cl = (0x001011 >> (4 * pr)) & 0xF;  // 1, 1, 0, 1, 0, 0
+                    cur.p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[li][h], bv[cl][h], i == 0 ? zero16 : cur.p,
+                                                                    0, 0, 0);
+                    constexpr int f0 = i < 8 ? 3 * i : 24 + 2 * (i - 8);
+                    constexpr int f1 = i < 8 ? f0 + 3 : f0 + 2;
+                    static_for<f1 - f0>([&](auto fc) { fold_op(old, f0 + decltype(fc)::value); });
+                    __builtin_amdgcn_sched_barrier(0);
+                });
+                barrier();
+            }
+        });
+    }
+    if (T & 1) {  // uniform: the last stage's products are in st_buf[(T - 1) % 2]
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int f = 0; f < 32; ++f) fold_op(st_buf[0], f);
+    } else {
 #pragma unroll
-            for (int tn = 0; tn < 2; ++tn) P[u][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[u][1], bl[u][tn], P[u][tn], 0, 0, 0);
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int tn = 0; tn < 2; ++tn) P[u][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[u][2], bh[u][tn], P[u][tn], 0, 0, 0);
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int tn = 0; tn < 2; ++tn) P[u][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[u][0], bl[u][tn], P[u][tn], 0, 0, 0);
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int tn = 0; tn < 2; ++tn) P[u][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[u][1], bh[u][tn], P[u][tn], 0, 0, 0);
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int tn = 0; tn < 2; ++tn) P[u][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[u][0], bh[u][tn], P[u][tn], 0, 0, 0);
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int tn = 0; tn < 2; ++tn)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[tn][i] = fma(nv[u][tn], static_cast<double>(P[u][tn][i]), acc[tn][i]);
-        barrier();
+        for (int f = 0; f < 32; ++f) fold_op(st_buf[1], f);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped copies past the last stage
+    // The two halves of K of each tile, added in double: the wavefront of sub-group u stores results
+    // 8 u .. 8 u + 7 of its tile and hands the other eight to its partner through LDS.
+    double* red = reinterpret_cast<double*>(&lds.a[0][0][0][0]);  // [4 tiles][16 results][64 lanes]
+    auto hand_over = [&](auto mine_c) {
+        constexpr int other = 8 - decltype(mine_c)::value;
 #pragma unroll
-    for (int tn = 0; tn < 2; ++tn) {
-        const int col = n0 + 16 * tn + j;
+        for (int v = 0; v < 8; ++v) red[((wid & 3) * 16 + other + v) * 64 + lane] = acc[other + v];
+    };
+    auto store = [&](auto mine_c) {
+        constexpr int mine = decltype(mine_c)::value;
+        const int col = nt0 + 32 * wn + col32;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = m0 + 4 * q + i;
-            if (row < Mi && col < N) c[static_cast<size_t>(row) * N + col] = float_to_half_bits(static_cast<float>(acc[tn][i]));
+        for (int v = mine; v < mine + 8; ++v) {
+            const int row = mt0 + 32 * wm + 8 * (v >> 2) + 4 * half + (v & 3);
+            const double s = acc[v] + red[((wid & 3) * 16 + v) * 64 + lane];
+            if (row < Mi && col < N) c[static_cast<size_t>(row) * N + col] = double_to_half_bits(s);
         }
-    }
+    };
+    __syncthreads();  // every wavefront is past its last read of lds.a, and every copy has landed
+    if (ku == 0)
+        hand_over(std::integral_constant<int, 0>{});
+    else
+        hand_over(std::integral_constant<int, 8>{});
+    __syncthreads();
+    if (ku == 0)
+        store(std::integral_constant<int, 0>{});
+    else
+        store(std::integral_constant<int, 8>{});
 }
 
 bool cq4_uses_mfma(const Cq4View& w, uint32_t m) {

@@ -12,6 +12,7 @@
 namespace spaceslug {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // v_cvt_off_f32_i4 reads bits 3..0 of its operand as a two's-complement value v

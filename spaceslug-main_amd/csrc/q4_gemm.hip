@@ -354,8 +354,6 @@ __host__ __device__ constexpr int wide_inflight(int first, int count) {
     return count == 0 ? 0 : wide_copies(first) + wide_inflight(first + 1, count - 1);
 }
 
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-
 // Tile order of the wide kernel: XCD-contiguous runs as in xcd_tile, over a linear order that
 // walks bands of kWideBandRows tile rows, each band column by column with its rows fastest. The
 // 32 CUs of an XCD then hold 2 tile rows x 16 tile columns at a time, whose operands per group
