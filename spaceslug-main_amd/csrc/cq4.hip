@@ -194,6 +194,139 @@ __global__ __launch_bounds__(256) void cq4_transform_hadamard_wave_kernel(Cq4Vie
     }
 }
 
+// Value of v in lane (this lane ^ MASK), MASK < 32, without LDS memory: DPP for masks 1 and 2
+// (quad permutes) and 8 (rotate by 8 within each row of 16 lanes), ds_swizzle for 4 and 16.
+template <int MASK>
+__device__ __forceinline__ float lane_xor(float v) {
+    const int x = __float_as_int(v);
+    int r;
+    if constexpr (MASK == 1)
+        r = __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);  // quad_perm [1, 0, 3, 2]
+    else if constexpr (MASK == 2)
+        r = __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);  // quad_perm [2, 3, 0, 1]
+    else if constexpr (MASK == 8)
+        r = __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false);  // row_ror:8
+    else
+        r = __builtin_amdgcn_ds_swizzle(x, 0x1F | (MASK << 10));  // bit mode: lane ^ MASK within 32
+    return __int_as_float(r);
+}
+
+// Hadamard basis written straight as bf16 limbs for the MFMA GEMM (group size GS = 64, 128 or 256;
+// activations and scales 16-byte aligned, signs 8-byte aligned): one wavefront per 512 consecutive
+// values of a row, lane l holding values 8 l .. 8 l + 7, so every load and limb store is 16 bytes
+// per lane. Butterflies of stride 1, 2 and 4 pair a lane's own values and strides 8 .. GS / 2 pair
+// lane l with lane l ^ (stride / 8): the operations and their order are those of
+// cq4_transform_hadamard_kernel (cactus_x86.cpp:56-66), so the values are identical. A group
+// never straddles the end of a row (GS divides K and 512), so lanes past the end exchange only
+// among themselves; they load nothing and store nothing. With a permutation the wavefront's
+// values pass through LDS for the gather.
+template <int GS>
+__global__ __launch_bounds__(256) void cq4_transform_hadamard_limbs_kernel(Cq4View w, const uint16_t* __restrict__ a,
+                                                                           uint16_t* __restrict__ xs, uint32_t M,
+                                                                           uint32_t chunks) {
+    __shared__ float gather[4][512];
+    const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const uint32_t unit = blockIdx.x * 4 + wv;  // row * chunks + chunk
+    if (unit >= M * chunks) return;             // whole wavefronts
+    const uint32_t K = w.K;
+    const uint32_t row = unit / chunks, k0 = (unit - row * chunks) * 512 + 8 * lane;
+    const bool live = k0 < K;
+    const uint32_t j0 = k0 & (GS - 1);  // position of the lane's first value in its group
+    u32x4 av = {0u, 0u, 0u, 0u}, sv = {0u, 0u, 0u, 0u};
+    uint2 lv = {0u, 0u}, rv = {0u, 0u};
+    u32x4 pv[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+    const uint16_t* sp = w.input_scale_recip ? w.input_scale_recip : w.input_scale;
+    if (live) {
+        av = *reinterpret_cast<const u32x4*>(a + static_cast<size_t>(row) * K + k0);
+        if (sp) sv = *reinterpret_cast<const u32x4*>(sp + k0);
+        if (w.left_signs) lv = *reinterpret_cast<const uint2*>(w.left_signs + j0);
+        if (w.permutation) {
+            pv[0] = *reinterpret_cast<const u32x4*>(w.permutation + j0);
+            pv[1] = *reinterpret_cast<const u32x4*>(w.permutation + j0 + 4);
+        } else if (w.right_signs) {
+            rv = *reinterpret_cast<const uint2*>(w.right_signs + j0);
+        }
+    }
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint16_t ah = static_cast<uint16_t>(av[e >> 1] >> (16 * (e & 1)));
+        const uint16_t sh = static_cast<uint16_t>(sv[e >> 1] >> (16 * (e & 1)));
+        // input_recip's value: the reciprocal as given, or 1 / scale, or 1
+        const float r = w.input_scale_recip ? half_bits_to_float(sh) : (w.input_scale ? 1.0f / half_bits_to_float(sh) : 1.0f);
+        const int8_t ls = static_cast<int8_t>((e < 4 ? lv.x : lv.y) >> (8 * (e & 3)));
+        const float sign = w.left_signs ? static_cast<float>(ls) : 1.0f;
+        v[e] = half_bits_to_float(ah) * r * sign;
+    }
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1)  // strides 1, 2, 4 within the lane
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            if ((e & h) == 0) {
+                const float x = v[e], y = v[e + h];
+                v[e] = x + y;
+                v[e + h] = x - y;
+            }
+    auto cross = [&](auto mask_c) {  // stride 8 mask: lane ^ mask holds the partner values
+        constexpr int mask = decltype(mask_c)::value;
+        const bool upper = (lane & mask) != 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float o = lane_xor<mask>(v[e]);
+            v[e] = upper ? o - v[e] : v[e] + o;
+        }
+    };
+    cross(std::integral_constant<int, 1>{});
+    cross(std::integral_constant<int, 2>{});
+    cross(std::integral_constant<int, 4>{});
+    if constexpr (GS >= 128) cross(std::integral_constant<int, 8>{});
+    if constexpr (GS >= 256) cross(std::integral_constant<int, 16>{});
+    const float inv = 1.0f / sqrtf(static_cast<float>(GS));
+    float x[8];
+    int8_t rs[8];
+    if (w.permutation) {  // uniform
+        float* g = &gather[wv][0];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) g[8 * lane + e] = v[e];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const uint32_t gbase = 8 * lane - j0;  // the group's first value in the wavefront's chunk
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            // an out-of-range entry is masked into the group (the host entry point rejects it)
+            const uint32_t src = pv[e >> 2][e & 3] & (GS - 1);
+            x[e] = g[gbase + src];
+            rs[e] = (w.right_signs && live) ? w.right_signs[src] : int8_t{1};
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            x[e] = v[e];
+            rs[e] = static_cast<int8_t>((e < 4 ? rv.x : rv.y) >> (8 * (e & 3)));
+        }
+    }
+    uint32_t limb[3][8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float sign = w.right_signs ? static_cast<float>(rs[e]) : 1.0f;
+        uint32_t b[3];
+        split_bf16_limbs(x[e] * inv * sign, b);
+#pragma unroll
+        for (int li = 0; li < 3; ++li) limb[li][e] = b[li];
+    }
+    if (live) {
+        uint16_t* d = xs + (static_cast<size_t>(row) * (K >> 6) + (k0 >> 6)) * (3 * 64) + (k0 & 63);
+#pragma unroll
+        for (int li = 0; li < 3; ++li) {
+            u32x4 o;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = limb[li][2 * i] | (limb[li][2 * i + 1] << 16);
+            *reinterpret_cast<u32x4*>(d + 64 * li) = o;
+        }
+    }
+}
+
 // Orthogonal basis: A_rot[m][i] = sum_k A[m][k] recip[k] R[k][i]; grid (ceil(K/256), M).
 __global__ __launch_bounds__(256) void cq4_transform_orthogonal_kernel(Cq4View w, const uint16_t* __restrict__ a,
                                                                        float* __restrict__ out, uint16_t* __restrict__ xs) {
@@ -593,11 +726,12 @@ constexpr int kCq4PipeWaves = 8;
 constexpr uint32_t kCq4NormsMax = 128;  // norm groups per column held in LDS
 
 struct Cq4PipeLds {
+    // first, so that ds_read's 16-bit offset field reaches both tables from one address
+    uint32_t lut[2][256];  // codebook limb (high, low), byte b: the limbs of entries b % 16 (low half) and b / 16
     u32x4 a[kCq4Stages][kCq4Limbs][8][64];   // as Cq4MfmaStage::a, per stage
     uint32_t braw[kCq4Stages][512];          // stage, thread: its packed word as copied
     u32x4 b[2][2][2][2][2][64];              // stage parity, sub-group, codebook limb, 32-column tile, half, slot
-    uint16_t norms[kCq4NormsMax][kCq4Tile];  // group, tile column (fp16 bits)
-    uint32_t lut[16];
+    uint16_t norms[kCq4Tile * kCq4NormsMax + 128];  // tile column, group (fp16 bits), as in the array; copy slack
 };
 static_assert(sizeof(Cq4PipeLds) <= 160 * 1024, "LDS budget");
 
@@ -654,52 +788,86 @@ __global__ __launch_bounds__(64 * kCq4PipeWaves) void cq4_gemm_pipe_kernel(Cq4Vi
                                              &lds.a[st][li][wid][0], 16, 0, 0);
         __builtin_amdgcn_global_load_lds(bsrc + 4 * (2 * t + bu), &lds.braw[st][64 * wid], 4, 0, 0);
     };
-    auto decode = [&](int t) {
-        const int st = t & (kCq4Stages - 1), par = t & 1;
-        const uint32_t wd = lds.braw[st][tid];
-        uint32_t e[8];
+    // Decode of stage t, in three steps laid into different MFMA windows: the packed word, its eight
+    // codebook entries, then the high and low limbs written to the stage's B buffer.
+    auto decode_word = [&](int t) { return lds.braw[t & (kCq4Stages - 1)][tid]; };
+    auto decode_lookup = [&](uint32_t wd, u32x4& hi, u32x4& lo) {  // one table entry per byte (two values)
 #pragma unroll
-        for (int k = 0; k < 8; ++k) e[k] = lds.lut[(wd >> (4 * k)) & 0xFu];
-        u32x4 hi, lo;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            hi[i] = __builtin_amdgcn_perm(e[2 * i + 1], e[2 * i], 0x05040100u);  // low halves
-            lo[i] = __builtin_amdgcn_perm(e[2 * i + 1], e[2 * i], 0x07060302u);  // high halves
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t b = (wd >> (8 * j)) & 0xFFu;
+            hi[j] = lds.lut[0][b];
+            lo[j] = lds.lut[1][b];
         }
-        lds.b[par][bu][0][bc >> 5][bw >> 1][bdst] = hi;
-        lds.b[par][bu][1][bc >> 5][bw >> 1][bdst] = lo;
+    };
+    auto decode_write = [&](int t, const u32x4& hi, const u32x4& lo) {
+        lds.b[t & 1][bu][0][bc >> 5][bw >> 1][bdst] = hi;
+        lds.b[t & 1][bu][1][bc >> 5][bw >> 1][bdst] = lo;
+    };
+    auto decode = [&](int t) {
+        u32x4 hi, lo;
+        decode_lookup(decode_word(t), hi, lo);
+        decode_write(t, hi, lo);
     };
     auto barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
+    // The tile's norms (copied as they lie: 64 columns of G values, contiguous), the codebook (an
+    // ordinary load), then stages 0 .. 3; stages 2 and 3 stay in flight while stages 0 and 1 are
+    // decoded and read: `s_waitcnt vmcnt(8)` below leaves exactly their 8 copies outstanding, as each
+    // iteration's wait does for the two youngest stages.
+    {
+        const char* nsrc = reinterpret_cast<const char*>(w.norms) + static_cast<size_t>(nt0) * G * 2;
+        const int units = kCq4Tile * G / 2;  // 4-byte units of the tile's norms
+        const size_t last = static_cast<size_t>(N - nt0) * G * 2 - 4;  // the last whole unit in the array
+        for (int b = wid; 64 * b < units; b += kCq4PipeWaves)  // uniform
+            __builtin_amdgcn_global_load_lds(nsrc + min(static_cast<size_t>(4 * (64 * b + lane)), last),
+                                             reinterpret_cast<char*>(lds.norms) + 256 * b, 4, 0, 0);
+    }
+    // the two codebook entries of this thread's table entry (byte tid % 256 of limb tid / 256)
+    const uint16_t cb_lo = w.codebook[tid & 15], cb_hi = w.codebook[(tid >> 4) & 15];
     issue(0, 0);
     issue(min(1, T - 1), 1);
     issue(min(2, T - 1), 2);
-    // Codebook and norms with ordinary loads, after the copies are on their way.
-    if (tid < 16) {
-        const float v = half_bits_to_float(w.codebook[tid]);
-        const uint32_t hi = __float_as_uint(v) & 0xFFFF0000u;
-        const float lo = v - __uint_as_float(hi);  // exact, at most 3 significant bits
-        lds.lut[tid] = (hi >> 16) | (__float_as_uint(lo) & 0xFFFF0000u);
+    issue(min(3, T - 1), 3);
+    // s_waitcnt vmcnt(8) through the builtin, so the compiler knows the codebook value (loaded
+    // before it) has arrived: this wavefront's norms, codebook value and stages 0 and 1 are in.
+    __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt 8, expcnt and lgkmcnt not waited for
+    {
+        // bf16 limbs of a codebook value: the high half of its fp32 form, and the exact remainder
+        // (at most 3 significant bits)
+        auto limb = [&](uint16_t h) {
+            const float v = half_bits_to_float(h);
+            const uint32_t hi = __float_as_uint(v) & 0xFFFF0000u;
+            return (tid >> 8) == 0 ? hi >> 16 : __float_as_uint(v - __uint_as_float(hi)) >> 16;
+        };
+        lds.lut[tid >> 8][tid & 255] = limb(cb_lo) | (limb(cb_hi) << 16);
     }
-    // two loads in flight per thread and pass (64 * G <= 8192 values: at most 8 passes)
-    for (int e0 = tid; e0 < kCq4Tile * G; e0 += 2 * 64 * kCq4PipeWaves) {
-        uint16_t v[2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int e = min(e0 + 64 * kCq4PipeWaves * i, kCq4Tile * G - 1);
-            const int col = e / G, g = e - col * G;
-            v[i] = w.norms[static_cast<size_t>(min(nt0 + col, N - 1)) * G + g];
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int e = e0 + 64 * kCq4PipeWaves * i;
-            if (e < kCq4Tile * G) lds.norms[e % G][e / G] = v[i];
-        }
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();  // lut visible
+    barrier();  // lut and norms visible, every wavefront's stages 0 and 1 copied
     decode(0);
+    decode(1);  // past the last stage: an unread buffer from a clamped copy
     barrier();
+
+    // MFMA operands of one stage in registers: activation limbs x halves, codebook limbs x halves.
+    struct Operands {
+        bf16x8 a[kCq4Limbs][2], b[2][2];
+    };
+    Operands ops[2];
+    // Operand reads of stage t, in the order the chain uses them: limb 2, codebook low, limb 1,
+    // codebook high, limb 0 (one pair per call, part 0 .. 4).
+    auto read_part = [&](Operands& o, int t, int part) {
+        const int sidx = t & (kCq4Stages - 1), par = t & 1;
+        if (part == 0 || part == 2 || part == 4) {
+            const int li = 2 - part / 2;
+            o.a[li][0] = __builtin_bit_cast(bf16x8, (&lds.a[sidx][li][0][0])[aidx0]);
+            o.a[li][1] = __builtin_bit_cast(bf16x8, (&lds.a[sidx][li][0][0])[aidx1]);
+        } else {
+            const int cl = part == 1 ? 1 : 0;
+            o.b[cl][0] = __builtin_bit_cast(bf16x8, lds.b[par][ku][cl][wn][0][bsrc0]);
+            o.b[cl][1] = __builtin_bit_cast(bf16x8, lds.b[par][ku][cl][wn][1][bsrc1]);
+        }
+    };
+#pragma unroll
+    for (int part = 0; part < 5; ++part) read_part(ops[0], 0, part);
+    barrier();  // stage 0's slot is read before iteration 0 copies into it
 
     f32x16 zero16;
 #pragma unroll
@@ -707,9 +875,6 @@ __global__ __launch_bounds__(64 * kCq4PipeWaves) void cq4_gemm_pipe_kernel(Cq4Vi
     double acc[16];
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[v] = 0.0;
-    // Chain step i (0 .. 11): activation limb, codebook limb (0 high, 1 low) and half, the
-    // products smallest first: (2, lo), (1, lo), (2, hi), (0, lo), (1, hi), (0, hi), each over
-    // both halves.
     struct Stage {
         f32x16 p;
         double norm;
@@ -734,6 +899,12 @@ __global__ __launch_bounds__(64 * kCq4PipeWaves) void cq4_gemm_pipe_kernel(Cq4Vi
         }
     };
 
+    // Iteration t: copies of stage t + 4 into slot t % 4 (stage t's operands are in registers), then
+    // the 12-MFMA chain of stage t with, between its MFMAs, the fold of stage t - 1, the operand
+    // reads of stage t + 1, stage t's norm, and the decode of stage t + 2 (after `s_waitcnt
+    // vmcnt(8)`: this wavefront's copies of stage t + 2 have landed, those of t + 3 and t + 4 may
+    // not have); then one barrier, after which every wavefront's copies of stage t + 2 and its
+    // decode are visible and every read of stage t + 1's slot is done.
     for (int t0 = 0; t0 < T; t0 += 2) {
         static_for<2>([&](auto uc) {
             constexpr int u = decltype(uc)::value;
@@ -741,32 +912,32 @@ __global__ __launch_bounds__(64 * kCq4PipeWaves) void cq4_gemm_pipe_kernel(Cq4Vi
             if (t < T) {  // uniform
                 Stage& cur = st_buf[u];
                 const Stage& old = st_buf[u ^ 1];
-                issue(min(t + 3, T - 1), (t + 3) & (kCq4Stages - 1));
-                const int sidx = t & (kCq4Stages - 1), par = t & 1;
-                bf16x8 av[kCq4Limbs][2], bv[2][2];
-#pragma unroll
-                for (int li = 0; li < kCq4Limbs; ++li) {
-                    av[li][0] = __builtin_bit_cast(bf16x8, (&lds.a[sidx][li][0][0])[aidx0]);
-                    av[li][1] = __builtin_bit_cast(bf16x8, (&lds.a[sidx][li][0][0])[aidx1]);
-                }
-#pragma unroll
-                for (int cl = 0; cl < 2; ++cl) {
-                    bv[cl][0] = __builtin_bit_cast(bf16x8, lds.b[par][ku][cl][wn][0][bsrc0]);
-                    bv[cl][1] = __builtin_bit_cast(bf16x8, lds.b[par][ku][cl][wn][1][bsrc1]);
-                }
-                cur.norm = static_cast<double>(half_bits_to_float(lds.norms[(2 * t + ku) / spg][32 * wn + col32]));
-                asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // this wavefront's copies of stage t + 1
-                decode(t + 1);  // past the last stage: rewrites an unread buffer from a clamped copy
+                const Operands& op = ops[u];
+                Operands& nxt = ops[u ^ 1];
+                issue(min(t + 4, T - 1), t & (kCq4Stages - 1));
+                uint32_t wd = 0;
+                u32x4 dhi, dlo;
+                uint16_t nraw = 0;
                 static_for<12>([&](auto ic) {
                     constexpr int i = decltype(ic)::value;
                     constexpr int pr = i >> 1, h = i & 1;
                     constexpr int li = (0x010212 >> (4 * pr)) & 0xF;  // 2, 1, 2, 0, 1, 0
                     constexpr int cl = (0x001011 >> (4 * pr)) & 0xF;  // 1, 1, 0, 1, 0, 0
-                    cur.p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[li][h], bv[cl][h], i == 0 ? zero16 : cur.p,
+                    cur.p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op.a[li][h], op.b[cl][h], i == 0 ? zero16 : cur.p,
                                                                     0, 0, 0);
+                    __builtin_amdgcn_sched_barrier(0);  // the MFMA first: a wait below stalls only the rest
                     constexpr int f0 = i < 8 ? 3 * i : 24 + 2 * (i - 8);
                     constexpr int f1 = i < 8 ? f0 + 3 : f0 + 2;
                     static_for<f1 - f0>([&](auto fc) { fold_op(old, f0 + decltype(fc)::value); });
+                    if constexpr (i < 5) read_part(nxt, t + 1, i);  // past the last stage: unused values
+                    if constexpr (i == 5) {
+                        nraw = lds.norms[(32 * wn + col32) * G + (2 * t + ku) / spg];
+                        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // this wavefront's copies of stage t + 2
+                        wd = decode_word(t + 2);
+                    }
+                    if constexpr (i == 6) decode_lookup(wd, dhi, dlo);
+                    if constexpr (i == 8) decode_write(t + 2, dhi, dlo);  // past the last stage: an unread buffer
+                    if constexpr (i == 9) cur.norm = static_cast<double>(half_bits_to_float(nraw));
                     __builtin_amdgcn_sched_barrier(0);
                 });
                 barrier();
@@ -781,35 +952,56 @@ __global__ __launch_bounds__(64 * kCq4PipeWaves) void cq4_gemm_pipe_kernel(Cq4Vi
         for (int f = 0; f < 32; ++f) fold_op(st_buf[1], f);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped copies past the last stage
-    // The two halves of K of each tile, added in double: the wavefront of sub-group u stores results
-    // 8 u .. 8 u + 7 of its tile and hands the other eight to its partner through LDS.
+    // The two halves of K of each tile, added in double: the wavefront of sub-group u finishes results
+    // 8 u .. 8 u + 7 of its tile and hands the other eight to its partner through LDS. The fp16 tile
+    // is then assembled in LDS and stored as one 16-byte row piece per thread.
     double* red = reinterpret_cast<double*>(&lds.a[0][0][0][0]);  // [4 tiles][16 results][64 lanes]
+    uint16_t* tile = reinterpret_cast<uint16_t*>(&lds.b[0][0][0][0][0][0]);  // [64 rows][64 columns]
     auto hand_over = [&](auto mine_c) {
         constexpr int other = 8 - decltype(mine_c)::value;
 #pragma unroll
         for (int v = 0; v < 8; ++v) red[((wid & 3) * 16 + other + v) * 64 + lane] = acc[other + v];
     };
-    auto store = [&](auto mine_c) {
+    auto finish = [&](auto mine_c) {
         constexpr int mine = decltype(mine_c)::value;
-        const int col = nt0 + 32 * wn + col32;
 #pragma unroll
         for (int v = mine; v < mine + 8; ++v) {
-            const int row = mt0 + 32 * wm + 8 * (v >> 2) + 4 * half + (v & 3);
+            const int row = 32 * wm + 8 * (v >> 2) + 4 * half + (v & 3);
             const double s = acc[v] + red[((wid & 3) * 16 + v) * 64 + lane];
-            if (row < Mi && col < N) c[static_cast<size_t>(row) * N + col] = double_to_half_bits(s);
+            tile[row * kCq4Tile + 32 * wn + col32] = double_to_half_bits(s);
         }
     };
-    __syncthreads();  // every wavefront is past its last read of lds.a, and every copy has landed
+    __syncthreads();  // every wavefront is past its last read of lds.a and lds.b, and every copy has landed
     if (ku == 0)
         hand_over(std::integral_constant<int, 0>{});
     else
         hand_over(std::integral_constant<int, 8>{});
     __syncthreads();
     if (ku == 0)
-        store(std::integral_constant<int, 0>{});
+        finish(std::integral_constant<int, 0>{});
     else
-        store(std::integral_constant<int, 8>{});
+        finish(std::integral_constant<int, 8>{});
+    __syncthreads();
+    {
+        const int rl = tid >> 3, c8 = 8 * (tid & 7);  // tile row, first of 8 columns
+        const int row = mt0 + rl, col = nt0 + c8;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(&tile[rl * kCq4Tile + c8]);
+        const bool vec = N % 8 == 0 && (reinterpret_cast<uintptr_t>(c) & 15) == 0;  // uniform
+        if (row < Mi) {
+            uint16_t* dst = c + static_cast<size_t>(row) * N + col;
+            if (vec && col + 8 <= N) {
+                *reinterpret_cast<u32x4*>(dst) = v;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (col + e < N) dst[e] = static_cast<uint16_t>(v[e >> 1] >> (16 * (e & 1)));
+            }
+        }
+    }
 }
+
+// A null pointer counts as aligned (the array is absent).
+bool aligned(const void* p, uintptr_t bytes) { return (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) == 0; }
 
 bool cq4_uses_mfma(const Cq4View& w, uint32_t m) {
     const bool orth = (w.flags & kCq4FlagOrthogonal) != 0;
@@ -851,6 +1043,17 @@ hipError_t launch_cq4_matmul(const Cq4View& w, const uint16_t* a, uint32_t m, ui
     if (orth) {
         hipLaunchKernelGGL(cq4_transform_orthogonal_kernel, dim3((w.K + 255) / 256, m), dim3(256), 0, stream, w, a,
                            ap, xs);
+    } else if (mfma && (w.group_size == 64 || w.group_size == 128 || w.group_size == 256) && aligned(a, 16) &&
+               aligned(w.input_scale_recip, 16) && aligned(w.input_scale, 16) && aligned(w.left_signs, 8) &&
+               aligned(w.right_signs, 8) && aligned(w.permutation, 16)) {
+        const uint32_t chunks = (w.K + 511) / 512;
+        const dim3 grid((m * chunks + 3) / 4);
+        if (w.group_size == 64)
+            hipLaunchKernelGGL(cq4_transform_hadamard_limbs_kernel<64>, grid, dim3(256), 0, stream, w, a, xs, m, chunks);
+        else if (w.group_size == 128)
+            hipLaunchKernelGGL(cq4_transform_hadamard_limbs_kernel<128>, grid, dim3(256), 0, stream, w, a, xs, m, chunks);
+        else
+            hipLaunchKernelGGL(cq4_transform_hadamard_limbs_kernel<256>, grid, dim3(256), 0, stream, w, a, xs, m, chunks);
     } else if (w.group_size == 64 || w.group_size == 128 || w.group_size == 256) {
         const uint32_t pairs = m * w.num_groups;
         const dim3 grid((pairs + 3) / 4);
@@ -870,7 +1073,8 @@ hipError_t launch_cq4_matmul(const Cq4View& w, const uint16_t* a, uint32_t m, ui
     const bool inter = (w.flags & kCq4FlagInterleaved4Row) != 0;
     if (mfma) {
         const uint32_t tiles_m = (m + kCq4Tile - 1) / kCq4Tile, tiles_n = (w.N + kCq4Tile - 1) / kCq4Tile;
-        if (ng <= kCq4NormsMax)
+        // the pipelined kernel copies the tile's norms in 4-byte units
+        if (ng <= kCq4NormsMax && (static_cast<size_t>(w.N) * ng) % 2 == 0 && aligned(w.norms, 4))
             hipLaunchKernelGGL(cq4_gemm_pipe_kernel, dim3(tiles_m * tiles_n), dim3(64 * kCq4PipeWaves), 0, stream, w,
                                xs, c, m, gs, ng, tiles_m);
         else

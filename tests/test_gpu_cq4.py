@@ -91,7 +91,8 @@ def test_random_matrices(session, gpu, case):
 # M >= 32 with 4-bit LSB-packed indices, group sizes that are multiples of 32 and K % 64 == 0 run
 # on the MFMA kernel: ragged row and column tiles, one to several groups per row, signs,
 # permutation, both input-scale forms, the orthogonal basis, and the reference benchmark's 1024^3
-# shape; K = 96 (not a multiple of 64) at M = 48 stays on the other kernel. Up to 128 norm groups
+# shape; K = 96 (not a multiple of 64) at M = 48 stays on the other kernel. K = 768 and 320 end
+# rows with a partial 512-value chunk of the vector transform. Up to 128 norm groups
 # per column the pipelined MFMA kernel runs, beyond that the single-stage one.
 MFMA_CASES = [dict(bits=4, K=512, N=200, group_size=128, m=70),
               dict(bits=4, K=96, N=50, group_size=32, m=48),
@@ -100,6 +101,8 @@ MFMA_CASES = [dict(bits=4, K=512, N=200, group_size=128, m=70),
               dict(bits=4, K=256, N=130, group_size=32, m=64),
               dict(bits=4, K=512, N=64, group_size=64, scale="none", m=129),
               dict(bits=4, K=1024, N=1024, group_size=128, m=1024),
+              dict(bits=4, K=768, N=100, group_size=128, signs=True, perm=True, m=40),  # K % 512 != 0
+              dict(bits=4, K=320, N=64, group_size=64, signs=True, scale="scale", m=35),
               dict(bits=4, K=4096, N=72, group_size=32, m=40),    # 128 norm groups: the most held in LDS
               dict(bits=4, K=8192, N=40, group_size=32, m=36)]    # 256 groups: the single-stage kernel
 
@@ -114,29 +117,66 @@ def test_random_matrices_mfma(session, gpu, case):
     check(session, W, A, m, f"mfma {MFMA_CASES[case]} m={m}")
 
 
-def test_device_entry_equals_host_entry(session, gpu):
+def device_struct(W, keep: dict):
+    """The matrix's arrays copied to cuda:0 (kept alive in `keep`) and its CQ4MatrixStruct."""
     import torch
 
     from spaceslug_amd.backend import CQ4MatrixStruct
-
-    note("cq4 device entry")
-    W, A, M = cq4.reference_fixture("cq4_hadamard_signs")
-    host = run(session, W, A, M)
-    dev = torch.device("cuda:0")
-    keep = {}
 
     def d(name):
         a = getattr(W, name)
         if a is None:
             return None
-        t = torch.from_numpy(np.ascontiguousarray(a).view(np.uint8).copy()).to(dev)
+        t = torch.from_numpy(np.ascontiguousarray(a).view(np.uint8).copy()).to("cuda:0")
         keep[name] = t
         return t.data_ptr()
 
-    s = CQ4MatrixStruct(W.bits, W.K, W.N, W.group_size, W.num_groups, W.flags, *(d(n) for n in cq4.ARRAYS), None, None)
-    a_t = torch.from_numpy(A.view(np.int16).copy()).to(dev)
-    c_t = torch.empty((M, W.N), dtype=torch.int16, device=dev)
+    return CQ4MatrixStruct(W.bits, W.K, W.N, W.group_size, W.num_groups, W.flags, *(d(n) for n in cq4.ARRAYS),
+                           None, None)
+
+
+def run_device(session, s, a_ptr: int, M: int, N: int) -> np.ndarray:
+    import torch
+
+    c_t = torch.empty((M, N), dtype=torch.int16, device="cuda:0")
     st = torch.cuda.current_stream()
-    session.cq4_matmul_device(s, a_t.data_ptr(), M, c_t.data_ptr(), st.cuda_stream)
+    session.cq4_matmul_device(s, a_ptr, M, c_t.data_ptr(), st.cuda_stream)
     st.synchronize()
-    assert np.array_equal(c_t.cpu().numpy().view(np.uint16), host)
+    return c_t.cpu().numpy().view(np.uint16)
+
+
+def test_device_entry_equals_host_entry(session, gpu):
+    import torch
+
+    note("cq4 device entry")
+    W, A, M = cq4.reference_fixture("cq4_hadamard_signs")
+    host = run(session, W, A, M)
+    keep = {}
+    s = device_struct(W, keep)
+    a_t = torch.from_numpy(A.view(np.int16).copy()).to("cuda:0")
+    assert np.array_equal(run_device(session, s, a_t.data_ptr(), M, W.N), host)
+
+
+@pytest.mark.parametrize("gs", [64, 128, 256])
+def test_transform_kernels_agree(session, gpu, gs):
+    """On the MFMA path the Hadamard transform runs as 16-byte vector loads and limb stores when the
+    activations are 16-byte aligned, and one wavefront per (row, group) otherwise (here: a pointer one
+    element into an allocation). Both perform the same operations in the same order, so the products
+    are bitwise equal."""
+    import torch
+
+    note(f"cq4 transform kernels agree gs={gs}")
+    rng = np.random.default_rng(70 + gs)
+    W = cq4.random_matrix(rng, bits=4, K=768, N=80, group_size=gs, signs=True, perm=True, scale="scale")
+    M = 40
+    A = cq4.f16(rng.uniform(-1, 1, (M, W.K)))
+    keep = {}
+    s = device_struct(W, keep)
+    a_t = torch.from_numpy(A.view(np.int16).copy()).to("cuda:0")
+    buf = torch.zeros(M * W.K + 1, dtype=torch.int16, device="cuda:0")
+    buf[1:] = a_t.reshape(-1)
+    aligned = run_device(session, s, a_t.data_ptr(), M, W.N)
+    shifted = run_device(session, s, buf.data_ptr() + 2, M, W.N)
+    assert np.array_equal(aligned, shifted)
+    ok, _ = within_fp16_rounding(aligned, cq4.matmul(W, A, M))
+    assert ok
