@@ -709,18 +709,22 @@ __global__ __launch_bounds__(256) void cq4_gemm_mfma_kernel(Cq4View w, const uin
 //   - lane l of a 32x32x16 MFMA holds A[row l % 32][k = 8 (l / 32) .. +7] and B[k = 8 (l / 32)
 //     .. +7][column l % 32], and result element v is row 8 (v / 4) + 4 (l / 32) + v % 4 of
 //     column l % 32 (one column per lane, one norm per stage);
-//   - every operand reaches LDS by global_load_lds, kCq4Stages stages deep: the activation limbs
-//     (wavefront w copies the 8-row block w of each limb, three 1 KiB copies) and the packed
-//     indices as copied (4 bytes per thread: the word this thread decodes, so a thread waits only
-//     for its own wavefront's copies), decoded one stage ahead into a double-buffered MFMA B layout
-//     (sub-group, codebook limb, 32-column tile, half, slot); the norms of the tile's 64 columns,
-//     all groups, are read once before the loop;
-//   - iteration t copies stage t + 3 into slot (t + 3) % 4, which no live stage holds (past the
-//     last stage the copied stage is clamped, so every wavefront issues the same 4 copies per
-//     stage and `s_waitcnt vmcnt(8)` leaves exactly the two younger stages in flight), reads stage
-//     t's operands, waits for stage t + 1, decodes it, runs stage t's MFMAs with stage t - 1's
-//     fold between them, and passes one barrier. The loop issues no other vector-memory
-//     instruction.
+//   - every operand reaches LDS by global_load_lds: the activation limbs kCq4Stages stages deep
+//     (wavefront w copies the 8-row block w of each limb, three 1 KiB copies per stage), the packed
+//     indices by stage pairs (each thread copies the two words it decodes, one per stage, so it waits
+//     only for its own wavefront's copies; a wavefront reads 8 columns x 32 contiguous bytes per
+//     stage), the tile's norms (all groups) and the codebook once before the loop; the codebook
+//     becomes two 256-entry tables (per byte of packed indices, the high or low bf16 limbs of its
+//     two entries), so a word decodes with four byte extractions and eight table reads;
+//   - iteration t copies stage t + 4 into slot t % 4 (its operands were read into registers in
+//     iteration t - 1), and on even t the pair of stages t + 4, t + 5, then runs stage t's chain
+//     with, between its MFMAs, stage t - 1's fold, the operand reads of stage t + 1 and the decode
+//     of stage t + 2 into a double-buffered MFMA B layout (sub-group, codebook limb, 32-column
+//     tile, half, slot), and passes one barrier. Past the last stage the copied stage is clamped,
+//     so every wavefront issues the same copies per iteration and `s_waitcnt vmcnt(8)` leaves
+//     exactly the two younger stages and one pair in flight. The loop issues no other
+//     vector-memory instruction;
+//   - the output tile is assembled in LDS and stored as 16-byte row pieces.
 constexpr int kCq4Stages = 4;
 constexpr int kCq4PipeWaves = 8;
 constexpr uint32_t kCq4NormsMax = 128;  // norm groups per column held in LDS
@@ -729,20 +733,24 @@ struct Cq4PipeLds {
     // first, so that ds_read's 16-bit offset field reaches both tables from one address
     uint32_t lut[2][256];  // codebook limb (high, low), byte b: the limbs of entries b % 16 (low half) and b / 16
     u32x4 a[kCq4Stages][kCq4Limbs][8][64];   // as Cq4MfmaStage::a, per stage
-    uint32_t braw[kCq4Stages][512];          // stage, thread: its packed word as copied
+    // stage-pair slot, wavefront w, stage of the pair, thread: the packed word the thread decodes
+    uint32_t braw[2][kCq4PipeWaves][2][64];
     u32x4 b[2][2][2][2][2][64];              // stage parity, sub-group, codebook limb, 32-column tile, half, slot
     uint16_t norms[kCq4Tile * kCq4NormsMax + 128];  // tile column, group (fp16 bits), as in the array; copy slack
 };
 static_assert(sizeof(Cq4PipeLds) <= 160 * 1024, "LDS budget");
 
 // Address of the B operand of lane slot s (column s % 32, word 2 half + s / 32 of the sub-group)
-// of half `half`: s ^ 4 ((s >> 5) & 1) ^ 8 half. gfx950 serves 128-bit LDS reads 16 lanes per cycle
-// (in a half-wavefront, the 4-lane chunks whose index has even popcount parity together, then the
-// odd ones) and 128-bit writes 16 consecutive lanes per cycle; two lanes of a cycle conflict when
-// their addresses agree modulo 256 bytes. With this map the MFMA operand reads (lane l reads slot l
-// of one half) and the decode writes (thread 4 c + w writes column c's word w to half w / 2, slot
-// c + 32 (w % 2)) both touch 16 distinct 16-byte bank groups per cycle.
-__device__ __forceinline__ int cq4_b_addr(int s, int half) { return s ^ (4 * ((s >> 5) & 1)) ^ (8 * half); }
+// of half `half` in sub-group `sub`'s buffer: s ^ 4 ((s >> 5) & 1) ^ 8 half ^ 2 sub. gfx950 serves
+// 128-bit LDS reads 16 lanes per cycle (in a half-wavefront, the 4-lane chunks whose index has even
+// popcount parity together, then the odd ones) and 128-bit writes 16 consecutive lanes per cycle; two
+// lanes of a cycle conflict when their addresses agree modulo 256 bytes. With this map the MFMA
+// operand reads (lane l reads slot l of one half of one sub-group) and the decode writes (lane l of
+// wavefront w writes word l % 4 of sub-group (l / 4) % 2 of column 8 w + l / 8 to half (l % 4) / 2,
+// slot column + 32 (l % 2)) both touch 16 distinct 16-byte bank groups per cycle.
+__device__ __forceinline__ int cq4_b_addr(int s, int half, int sub) {
+    return s ^ (4 * ((s >> 5) & 1)) ^ (8 * half) ^ (2 * sub);
+}
 
 __global__ __launch_bounds__(64 * kCq4PipeWaves) void cq4_gemm_pipe_kernel(Cq4View w, const uint16_t* __restrict__ xs,
                                                                           uint16_t* __restrict__ c, uint32_t M,
@@ -767,30 +775,41 @@ __global__ __launch_bounds__(64 * kCq4PipeWaves) void cq4_gemm_pipe_kernel(Cq4Vi
         const int row_t = 2 * pair + ((lane >> 3) & 1);
         asrc = xs + static_cast<size_t>(min(mt0 + row_t, Mi - 1)) * T * (kCq4Limbs * 64) + 8 * ((lane & 7) ^ (pair & 7));
     }
-    // Packed-index word of this thread: sub-group bu, tile column bc, word bw.
-    const int bu = tid >> 8, bc = (tid >> 2) & 63, bw = tid & 3;
-    const uint32_t* bsrc =
-        reinterpret_cast<const uint32_t*>(w.packed + static_cast<size_t>(min(nt0 + bc, N - 1)) * (K >> 1)) + bw;
-    const int bdst = cq4_b_addr((bc & 31) + 32 * (bw & 1), bw >> 1);
+    // Packed-index word this thread decodes: sub-group bu, tile column bc, word bw.
+    const int bc = 8 * wid + (lane >> 3), bu = (lane >> 2) & 1, bw = lane & 3;
+    const int bdst = cq4_b_addr((bc & 31) + 32 * (bw & 1), bw >> 1, bu);
+    // This thread copies the packed words it decodes (so it waits only for its own wavefront's
+    // copies): per stage pair, words (lane % 8) of column bc for both stages, 32 contiguous bytes per
+    // column and stage.
+    const char* bsrc = reinterpret_cast<const char*>(w.packed) + static_cast<size_t>(min(nt0 + bc, N - 1)) * (K >> 1) +
+                       4 * (lane & 7);
     // This lane's A operand: row 32 wm + (lane & 31), chunk 4 ku + 2 h + (lane >> 5) of a stage for
     // half h (the layout of Cq4MfmaStage::a).
     const int ar = 32 * wm + col32;
     const int apr = ar >> 1;
     const int aidx0 = apr * 16 + 8 * (ar & 1) + ((4 * ku + half) ^ (apr & 7));
     const int aidx1 = apr * 16 + 8 * (ar & 1) + ((4 * ku + 2 + half) ^ (apr & 7));
-    const int bsrc0 = cq4_b_addr(lane, 0), bsrc1 = cq4_b_addr(lane, 1);
+    const int bsrc0 = cq4_b_addr(lane, 0, ku), bsrc1 = cq4_b_addr(lane, 1, ku);
 
-    // Stage t's copies into stage slot st (past the last stage, t is clamped and st is not).
+    // Stage t's activation limbs into stage slot st (past the last stage, t is clamped and st is not).
     auto issue = [&](int t, int st) {
 #pragma unroll
         for (int li = 0; li < kCq4Limbs; ++li)
             __builtin_amdgcn_global_load_lds(asrc + static_cast<size_t>(t) * (kCq4Limbs * 64) + li * 64,
                                              &lds.a[st][li][wid][0], 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(bsrc + 4 * (2 * t + bu), &lds.braw[st][64 * wid], 4, 0, 0);
+    };
+    // Packed indices of stages 2 j and 2 j + 1 into slot `slot`, one copy per stage (each wavefront
+    // reads 8 columns x 32 bytes). Past the end of a row (an odd stage count) the stage is clamped
+    // to the last.
+    auto issue_b = [&](int j, int slot) {
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc)
+            __builtin_amdgcn_global_load_lds(bsrc + min(32 * (2 * j + cc), (K >> 1) - 32), &lds.braw[slot][wid][cc][0], 4,
+                                             0, 0);
     };
     // Decode of stage t, in three steps laid into different MFMA windows: the packed word, its eight
     // codebook entries, then the high and low limbs written to the stage's B buffer.
-    auto decode_word = [&](int t) { return lds.braw[t & (kCq4Stages - 1)][tid]; };
+    auto decode_word = [&](int t) { return lds.braw[(t >> 1) & 1][wid][t & 1][lane]; };
     auto decode_lookup = [&](uint32_t wd, u32x4& hi, u32x4& lo) {  // one table entry per byte (two values)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -822,28 +841,41 @@ __global__ __launch_bounds__(64 * kCq4PipeWaves) void cq4_gemm_pipe_kernel(Cq4Vi
             __builtin_amdgcn_global_load_lds(nsrc + min(static_cast<size_t>(4 * (64 * b + lane)), last),
                                              reinterpret_cast<char*>(lds.norms) + 256 * b, 4, 0, 0);
     }
-    // the two codebook entries of this thread's table entry (byte tid % 256 of limb tid / 256)
-    const uint16_t cb_lo = w.codebook[tid & 15], cb_hi = w.codebook[(tid >> 4) & 15];
+    // The two codebook entries of this thread's table entry (byte tid % 256 of limb tid / 256). Loaded
+    // through asm, which the compiler's wait insertion does not follow (it would otherwise wait for every
+    // copy issued after them); the explicit vmcnt wait below covers them.
+    uint32_t cb_lo, cb_hi;
+    asm volatile("global_load_ushort %0, %1, off" : "=v"(cb_lo) : "v"(w.codebook + (tid & 15)) : "memory");
+    asm volatile("global_load_ushort %0, %1, off" : "=v"(cb_hi) : "v"(w.codebook + ((tid >> 4) & 15)) : "memory");
+    const int jmax = (T - 1) / 2;  // the last stage pair
     issue(0, 0);
+    issue_b(0, 0);
     issue(min(1, T - 1), 1);
     issue(min(2, T - 1), 2);
+    issue_b(min(1, jmax), 1);
     issue(min(3, T - 1), 3);
-    // s_waitcnt vmcnt(8) through the builtin, so the compiler knows the codebook value (loaded
-    // before it) has arrived: this wavefront's norms, codebook value and stages 0 and 1 are in.
-    __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt 8, expcnt and lgkmcnt not waited for
+    // this wavefront's norms, codebook values, stages 0 and 1 and pair 0 are in; stages 2 and 3 (3
+    // copies each) and pair 1 (2) may not be
+    asm volatile("s_waitcnt vmcnt(8)" : "+v"(cb_lo), "+v"(cb_hi) :: "memory");  // the values are in from here
     {
-        // bf16 limbs of a codebook value: the high half of its fp32 form, and the exact remainder
-        // (at most 3 significant bits)
+        // The bf16 limbs of a codebook value are the high half of its fp32 form and the exact
+        // remainder (at most 3 significant bits).
         auto limb = [&](uint16_t h) {
             const float v = half_bits_to_float(h);
             const uint32_t hi = __float_as_uint(v) & 0xFFFF0000u;
             return (tid >> 8) == 0 ? hi >> 16 : __float_as_uint(v - __uint_as_float(hi)) >> 16;
         };
-        lds.lut[tid >> 8][tid & 255] = limb(cb_lo) | (limb(cb_hi) << 16);
+        lds.lut[tid >> 8][tid & 255] = limb(static_cast<uint16_t>(cb_lo)) | (limb(static_cast<uint16_t>(cb_hi)) << 16);
     }
-    barrier();  // lut and norms visible, every wavefront's stages 0 and 1 copied
-    decode(0);
-    decode(1);  // past the last stage: an unread buffer from a clamped copy
+    barrier();  // norms and tables visible, every wavefront's stages 0 and 1 and pair 0 copied
+    {
+        u32x4 hi0, lo0, hi1, lo1;
+        const uint32_t w0 = decode_word(0), w1 = decode_word(1);
+        decode_lookup(w0, hi0, lo0);
+        decode_lookup(w1, hi1, lo1);
+        decode_write(0, hi0, lo0);
+        decode_write(1, hi1, lo1);  // past the last stage: an unread buffer from a clamped copy
+    }
     barrier();
 
     // MFMA operands of one stage in registers: activation limbs x halves, codebook limbs x halves.
@@ -899,12 +931,13 @@ __global__ __launch_bounds__(64 * kCq4PipeWaves) void cq4_gemm_pipe_kernel(Cq4Vi
         }
     };
 
-    // Iteration t: copies of stage t + 4 into slot t % 4 (stage t's operands are in registers), then
-    // the 12-MFMA chain of stage t with, between its MFMAs, the fold of stage t - 1, the operand
-    // reads of stage t + 1, stage t's norm, and the decode of stage t + 2 (after `s_waitcnt
-    // vmcnt(8)`: this wavefront's copies of stage t + 2 have landed, those of t + 3 and t + 4 may
-    // not have); then one barrier, after which every wavefront's copies of stage t + 2 and its
-    // decode are visible and every read of stage t + 1's slot is done.
+    // Iteration t: copies of stage t + 4 into slot t % 4 (stage t's operands are in registers) and on
+    // even t of the pair t + 4, t + 5, then the 12-MFMA chain of stage t with, between its MFMAs, the
+    // fold of stage t - 1, the operand reads of stage t + 1, stage t's norm, and the decode of stage
+    // t + 2 (after `s_waitcnt vmcnt(8)`: this wavefront's copies of stage t + 2 and of its pair have
+    // landed; stages t + 3 and t + 4 and the youngest pair may not have); then one barrier, after
+    // which every wavefront's copies of stage t + 2 and its decode are visible and every read of
+    // stage t + 1's slot is done.
     for (int t0 = 0; t0 < T; t0 += 2) {
         static_for<2>([&](auto uc) {
             constexpr int u = decltype(uc)::value;
@@ -915,6 +948,7 @@ __global__ __launch_bounds__(64 * kCq4PipeWaves) void cq4_gemm_pipe_kernel(Cq4Vi
                 const Operands& op = ops[u];
                 Operands& nxt = ops[u ^ 1];
                 issue(min(t + 4, T - 1), t & (kCq4Stages - 1));
+                if constexpr (u == 0) issue_b(min(t / 2 + 2, jmax), (t / 2) & 1);  // t is even
                 uint32_t wd = 0;
                 u32x4 dhi, dlo;
                 uint16_t nraw = 0;
@@ -932,7 +966,9 @@ __global__ __launch_bounds__(64 * kCq4PipeWaves) void cq4_gemm_pipe_kernel(Cq4Vi
                     if constexpr (i < 5) read_part(nxt, t + 1, i);  // past the last stage: unused values
                     if constexpr (i == 5) {
                         nraw = lds.norms[(32 * wn + col32) * G + (2 * t + ku) / spg];
-                        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // this wavefront's copies of stage t + 2
+                        // this wavefront's copies of stage t + 2 and of its pair; after them come stages
+                        // t + 3, t + 4 and one pair (3 + 3 + 2 copies)
+                        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
                         wd = decode_word(t + 2);
                     }
                     if constexpr (i == 6) decode_lookup(wd, dhi, dlo);
