@@ -829,10 +829,10 @@ __global__ __launch_bounds__(64 * kCq4PipeWaves) void cq4_gemm_pipe_kernel(Cq4Vi
     };
     auto barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
-    // The tile's norms (copied as they lie: 64 columns of G values, contiguous), the codebook (an
-    // ordinary load), then stages 0 .. 3; stages 2 and 3 stay in flight while stages 0 and 1 are
-    // decoded and read: `s_waitcnt vmcnt(8)` below leaves exactly their 8 copies outstanding, as each
-    // iteration's wait does for the two youngest stages.
+    // The tile's norms (copied as they lie: 64 columns of G values, contiguous), the codebook, then
+    // stages 0 .. 3 and pairs 0 and 1; stages 2 and 3 and pair 1 stay in flight while stages 0 and 1
+    // are decoded and read: `s_waitcnt vmcnt(8)` below leaves exactly their 3 + 3 + 2 copies
+    // outstanding, as each iteration's wait does.
     {
         const char* nsrc = reinterpret_cast<const char*>(w.norms) + static_cast<size_t>(nt0) * G * 2;
         const int units = kCq4Tile * G / 2;  // 4-byte units of the tile's norms
