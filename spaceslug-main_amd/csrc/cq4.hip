@@ -811,11 +811,15 @@ __global__ __launch_bounds__(64 * kCq4PipeWaves) void cq4_gemm_pipe_kernel(Cq4Vi
     // codebook entries, then the high and low limbs written to the stage's B buffer.
     auto decode_word = [&](int t) { return lds.braw[(t >> 1) & 1][wid][t & 1][lane]; };
     auto decode_lookup = [&](uint32_t wd, u32x4& hi, u32x4& lo) {  // one table entry per byte (two values)
+        // volatile: eight single reads straight into the two result vectors (paired reads of both
+        // tables would need register moves, and a wait for them, before the writes)
+        typedef __attribute__((address_space(3))) const volatile uint32_t lds_word;
+        lds_word* lut = (lds_word*)(&lds.lut[0][0]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const uint32_t b = (wd >> (8 * j)) & 0xFFu;
-            hi[j] = lds.lut[0][b];
-            lo[j] = lds.lut[1][b];
+            hi[j] = lut[b];
+            lo[j] = lut[256 + b];
         }
     };
     auto decode_write = [&](int t, const u32x4& hi, const u32x4& lo) {
@@ -963,16 +967,20 @@ __global__ __launch_bounds__(64 * kCq4PipeWaves) void cq4_gemm_pipe_kernel(Cq4Vi
                     constexpr int f0 = i < 8 ? 3 * i : 24 + 2 * (i - 8);
                     constexpr int f1 = i < 8 ? f0 + 3 : f0 + 2;
                     static_for<f1 - f0>([&](auto fc) { fold_op(old, f0 + decltype(fc)::value); });
-                    if constexpr (i < 5) read_part(nxt, t + 1, i);  // past the last stage: unused values
-                    if constexpr (i == 5) {
-                        nraw = lds.norms[(32 * wn + col32) * G + (2 * t + ku) / spg];
+                    // LDS reads complete in issue order, so the decode's reads go first: its waits
+                    // (for the packed word, then for the table entries) do not wait for the operand
+                    // reads behind them.
+                    if constexpr (i == 0) {
                         // this wavefront's copies of stage t + 2 and of its pair; after them come stages
                         // t + 3, t + 4 and one pair (3 + 3 + 2 copies)
                         asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
                         wd = decode_word(t + 2);
+                        nraw = lds.norms[(32 * wn + col32) * G + (2 * t + ku) / spg];
                     }
-                    if constexpr (i == 6) decode_lookup(wd, dhi, dlo);
-                    if constexpr (i == 8) decode_write(t + 2, dhi, dlo);  // past the last stage: an unread buffer
+                    if constexpr (i == 1) decode_lookup(wd, dhi, dlo);
+                    if constexpr (i >= 2 && i < 7) read_part(nxt, t + 1, i - 2);  // past the last stage: unused
+                    // the compiler waits for every LDS read before the writes; late, they are all in
+                    if constexpr (i == 10) decode_write(t + 2, dhi, dlo);  // past the last stage: an unread buffer
                     if constexpr (i == 9) cur.norm = static_cast<double>(half_bits_to_float(nraw));
                     __builtin_amdgcn_sched_barrier(0);
                 });
