@@ -103,6 +103,8 @@ MFMA_CASES = [dict(bits=4, K=512, N=200, group_size=128, m=70),
               dict(bits=4, K=1024, N=1024, group_size=128, m=1024),
               dict(bits=4, K=768, N=100, group_size=128, signs=True, perm=True, m=40),  # K % 512 != 0
               dict(bits=4, K=320, N=64, group_size=64, signs=True, scale="scale", m=35),
+              dict(bits=4, K=320, N=70, group_size=64, signs=True, scale="scale", m=500),
+              dict(bits=4, K=1024, N=96, group_size=256, signs=True, perm=True, scale="scale", m=512),
               dict(bits=4, K=4096, N=72, group_size=32, m=40),    # 128 norm groups: the most held in LDS
               dict(bits=4, K=8192, N=40, group_size=32, m=36)]    # 256 groups: the single-stage kernel
 
@@ -157,18 +159,17 @@ def test_device_entry_equals_host_entry(session, gpu):
     assert np.array_equal(run_device(session, s, a_t.data_ptr(), M, W.N), host)
 
 
-@pytest.mark.parametrize("gs", [64, 128, 256])
-def test_transform_kernels_agree(session, gpu, gs):
+@pytest.mark.parametrize("gs,M", [(64, 40), (128, 40), (256, 40), (128, 500), (256, 1000)])
+def test_transform_kernels_agree(session, gpu, gs, M):
     """On the MFMA path the Hadamard transform runs as 16-byte vector loads and limb stores when the
     activations are 16-byte aligned, and one wavefront per (row, group) otherwise (here: a pointer one
     element into an allocation). Both perform the same operations in the same order, so the products
     are bitwise equal."""
     import torch
 
-    note(f"cq4 transform kernels agree gs={gs}")
-    rng = np.random.default_rng(70 + gs)
+    note(f"cq4 transform kernels agree gs={gs} M={M}")
+    rng = np.random.default_rng(70 + gs + M)
     W = cq4.random_matrix(rng, bits=4, K=768, N=80, group_size=gs, signs=True, perm=True, scale="scale")
-    M = 40
     A = cq4.f16(rng.uniform(-1, 1, (M, W.K)))
     keep = {}
     s = device_struct(W, keep)
@@ -180,3 +181,24 @@ def test_transform_kernels_agree(session, gpu, gs):
     assert np.array_equal(aligned, shifted)
     ok, _ = within_fp16_rounding(aligned, cq4.matmul(W, A, M))
     assert ok
+
+
+def test_device_calls_in_a_row(session, gpu):
+    """Three device calls in a row at 1024 x 1024 x 1024 on the shared workspace, with different
+    activations: each matches the host entry bit for bit and the oracle to the fp16 bar (a call that
+    read a stale part of the workspace would carry the previous call's activations)."""
+    import torch
+
+    note("cq4 device entry: three calls in a row")
+    rng = np.random.default_rng(4242)
+    W = cq4.random_matrix(rng, bits=4, K=1024, N=1024, group_size=128)
+    M = 1024
+    keep = {}
+    s = device_struct(W, keep)
+    for call in range(3):
+        A = cq4.f16(rng.uniform(-1, 1, (M, W.K)))
+        a_t = torch.from_numpy(A.view(np.int16).copy()).to("cuda:0")
+        dev = run_device(session, s, a_t.data_ptr(), M, W.N)
+        assert np.array_equal(dev, run(session, W, A, M)), call
+        ok, _ = within_fp16_rounding(dev, cq4.matmul(W, A, M))
+        assert ok, call
