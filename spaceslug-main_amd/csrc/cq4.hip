@@ -220,16 +220,31 @@ __device__ __forceinline__ float lane_xor(float v) {
 // never straddles the end of a row (GS divides K and 512), so lanes past the end exchange only
 // among themselves; they load nothing and store nothing. With a permutation the wavefront's
 // values pass through LDS for the gather.
+//
+// With xcd_rows set (the GEMM's row tiles a multiple of 8), workgroup b works on the rows of 64-row
+// tiles t with t % 8 == b % 8: workgroups run on XCD b % 8, and the GEMM reads row tile t on XCD
+// t % 8, so each row's limbs are written through the L2 that later serves them.
 template <int GS>
 __global__ __launch_bounds__(256) void cq4_transform_hadamard_limbs_kernel(Cq4View w, const uint16_t* __restrict__ a,
                                                                            uint16_t* __restrict__ xs, uint32_t M,
-                                                                           uint32_t chunks) {
+                                                                           uint32_t chunks, bool xcd_rows) {
     __shared__ float gather[4][512];
     const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const uint32_t unit = blockIdx.x * 4 + wv;  // row * chunks + chunk
-    if (unit >= M * chunks) return;             // whole wavefronts
+    uint32_t row, chunk;
+    if (xcd_rows) {
+        const uint32_t unit = (blockIdx.x / 8) * 4 + wv;  // within XCD lane blockIdx % 8
+        const uint32_t lr = unit / chunks;
+        row = (blockIdx.x % 8 + 8 * (lr / 64)) * 64 + lr % 64;
+        chunk = unit - lr * chunks;
+        if (row >= M) return;  // whole wavefronts
+    } else {
+        const uint32_t unit = blockIdx.x * 4 + wv;  // row * chunks + chunk
+        if (unit >= M * chunks) return;             // whole wavefronts
+        row = unit / chunks;
+        chunk = unit - row * chunks;
+    }
     const uint32_t K = w.K;
-    const uint32_t row = unit / chunks, k0 = (unit - row * chunks) * 512 + 8 * lane;
+    const uint32_t k0 = chunk * 512 + 8 * lane;
     const bool live = k0 < K;
     const uint32_t j0 = k0 & (GS - 1);  // position of the lane's first value in its group
     u32x4 av = {0u, 0u, 0u, 0u}, sv = {0u, 0u, 0u, 0u};
@@ -1091,13 +1106,19 @@ hipError_t launch_cq4_matmul(const Cq4View& w, const uint16_t* a, uint32_t m, ui
                aligned(w.input_scale_recip, 16) && aligned(w.input_scale, 16) && aligned(w.left_signs, 8) &&
                aligned(w.right_signs, 8) && aligned(w.permutation, 16)) {
         const uint32_t chunks = (w.K + 511) / 512;
-        const dim3 grid((m * chunks + 3) / 4);
+        const uint32_t tiles_m = (m + kCq4Tile - 1) / kCq4Tile;
+        const bool xcd_rows = tiles_m % 8 == 0;  // the GEMM then reads row tile t on XCD t % 8
+        // XCD lane x holds tiles_m / 8 row tiles of 64 rows (the last may be partial)
+        const dim3 grid(xcd_rows ? 8 * ((tiles_m / 8 * kCq4Tile * chunks + 3) / 4) : (m * chunks + 3) / 4);
         if (w.group_size == 64)
-            hipLaunchKernelGGL(cq4_transform_hadamard_limbs_kernel<64>, grid, dim3(256), 0, stream, w, a, xs, m, chunks);
+            hipLaunchKernelGGL(cq4_transform_hadamard_limbs_kernel<64>, grid, dim3(256), 0, stream, w, a, xs, m, chunks,
+                               xcd_rows);
         else if (w.group_size == 128)
-            hipLaunchKernelGGL(cq4_transform_hadamard_limbs_kernel<128>, grid, dim3(256), 0, stream, w, a, xs, m, chunks);
+            hipLaunchKernelGGL(cq4_transform_hadamard_limbs_kernel<128>, grid, dim3(256), 0, stream, w, a, xs, m, chunks,
+                               xcd_rows);
         else
-            hipLaunchKernelGGL(cq4_transform_hadamard_limbs_kernel<256>, grid, dim3(256), 0, stream, w, a, xs, m, chunks);
+            hipLaunchKernelGGL(cq4_transform_hadamard_limbs_kernel<256>, grid, dim3(256), 0, stream, w, a, xs, m, chunks,
+                               xcd_rows);
     } else if (w.group_size == 64 || w.group_size == 128 || w.group_size == 256) {
         const uint32_t pairs = m * w.num_groups;
         const dim3 grid((pairs + 3) / 4);
