@@ -3,16 +3,16 @@
 // cactus_x86.cpp:133-240, 384-397); the reference's GPU chain is three
 // dispatches through two fp16 intermediates (transform_act -> dequant_w ->
 // sgemm_f16_am, vulkan-runtime/tests/test_cq4.cpp:255-334). Here:
-//   1. the activation transform writes the code-basis activations A' in fp32
-//      (one workgroup per (row, group) for the Hadamard basis: scale and left
-//      sign, an in-LDS normalized Walsh-Hadamard transform, right sign and
-//      permutation; a direct product with the rotation for the orthogonal mode),
-//      or, for the MFMA GEMM, each value as three exact bf16 limbs;
-//   2. one GEMM kernel decodes the packed indices in registers (LSB-first bit
+//   1. the activation transform writes the code-basis activations A' (scale and
+//      left sign, a normalized Walsh-Hadamard transform per group, right sign and
+//      permutation; a direct product with the rotation for the orthogonal mode):
+//      in fp32 for the VALU GEMMs, or, for the MFMA GEMMs, each value as three
+//      exact bf16 limbs;
+//   2. one GEMM kernel decodes the packed indices on the fly (LSB-first bit
 //      packing or 4-row interleaved panels), looks codebook values up in LDS and
-//      accumulates in fp32 per group, scaling each group sum by its norm; the
-//      dequantized weight matrix is never materialized, and C is rounded to fp16
-//      once.
+//      sums products in fp32 over at most 32 values, folding each sum times its
+//      group's norm in float64; the dequantized weight matrix is never
+//      materialized, and C is rounded to fp16 once.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
