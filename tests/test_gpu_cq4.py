@@ -106,7 +106,10 @@ MFMA_CASES = [dict(bits=4, K=512, N=200, group_size=128, m=70),
               dict(bits=4, K=320, N=70, group_size=64, signs=True, scale="scale", m=500),
               dict(bits=4, K=1024, N=96, group_size=256, signs=True, perm=True, scale="scale", m=512),
               dict(bits=4, K=4096, N=72, group_size=32, m=40),    # 128 norm groups: the most held in LDS
-              dict(bits=4, K=8192, N=40, group_size=32, m=36)]    # 256 groups: the single-stage kernel
+              dict(bits=4, K=8192, N=40, group_size=32, m=36),    # 256 groups: the single-stage kernel
+              dict(bits=4, K=64, N=80, group_size=64, m=40),      # one 64-value stage: every copy clamped
+              dict(bits=4, K=64, N=64, group_size=32, signs=True, scale="scale", m=64),
+              dict(bits=4, K=128, N=136, group_size=128, perm=True, m=97)]  # two stages, one stage pair
 
 
 @pytest.mark.parametrize("case", range(len(MFMA_CASES)))
