@@ -445,6 +445,64 @@ __global__ __launch_bounds__(256) void cq4_gemm_kernel(Cq4View w, const float* _
         if (m0 + r < M) c[static_cast<size_t>(m0 + r) * w.N + n] = double_to_half_bits(acc[r]);
 }
 
+// Index word wi (8 indices, all in group wi / wpg) of column n, and the flat index of its norm.
+// LSB-first: the column's group g is ng-major, its word cw at byte 4 cw; interleaved: row n & 3
+// of panel n / 4, its word cw at byte 16 cw + 4 (n & 3).
+template <bool INTER>
+__device__ __forceinline__ uint32_t cq4_gemv_word(const Cq4View& w, uint32_t n, uint32_t wi, uint32_t wpg,
+                                                  uint32_t ng, size_t& ni) {
+    const uint32_t g = wi / wpg, cw = wi % wpg;
+    const size_t pgb = static_cast<size_t>(wpg) * 4;  // bytes of one row's group
+    if constexpr (INTER) {
+        const size_t panel = static_cast<size_t>(n >> 2) * ng + g;
+        ni = panel * 4 + (n & 3);
+        return *reinterpret_cast<const uint32_t*>(w.packed + panel * 4 * pgb + (n & 3) * 4 + 16 * cw);
+    } else {
+        const size_t grp = static_cast<size_t>(n) * ng + g;
+        ni = grp;
+        return *reinterpret_cast<const uint32_t*>(w.packed + grp * pgb + 4 * cw);
+    }
+}
+
+// One index word against ROWS activation rows: 8 codebook lookups, per row an fp32 sum of the
+// 8 products, and acc[r] += norm * sum in float64.
+template <int ROWS, bool INTER>
+__device__ __forceinline__ void cq4_gemv_step(const float* lut, uint32_t word, uint16_t norm_bits,
+                                              const float* const (&arow)[ROWS], uint32_t wi, double (&acc)[ROWS]) {
+    float cv[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) cv[t] = lut[(word >> (4 * t)) & 0xFu];
+    const double norm = static_cast<double>(half_bits_to_float(norm_bits));
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        const f32x4_t lo = *reinterpret_cast<const f32x4_t*>(arow[r] + 8 * wi);
+        const f32x4_t hi = *reinterpret_cast<const f32x4_t*>(arow[r] + 8 * wi + 4);
+        const float av[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        float sum = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            // nibble t holds k = 8 cw + t (LSB) or 8 cw + (t >> 1) + 4 (t & 1) (interleaved)
+            const int kk = INTER ? (t >> 1) + 4 * (t & 1) : t;
+            sum = fmaf(av[kk], cv[t], sum);
+        }
+        acc[r] = fma(norm, static_cast<double>(sum), acc[r]);
+    }
+}
+
+// The 64 lane sums of each row reduced in float64 across the wavefront, rounded to fp16 once.
+template <int ROWS>
+__device__ __forceinline__ void cq4_gemv_store(double (&acc)[ROWS], uint16_t* c, uint32_t N, uint32_t M, uint32_t n,
+                                               uint32_t lane) {
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) acc[r] += __shfl_xor(acc[r], off);
+    if (lane == 0)
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r)
+            if (static_cast<uint32_t>(r) < M) c[static_cast<size_t>(r) * N + n] = double_to_half_bits(acc[r]);
+}
+
 // Up to 4 rows with 4-bit indices in either layout and word-aligned groups
 // (group size a multiple of 8): one wavefront per column, lane l taking the column's
 // 32-bit index words l, l + 64, ... (8 values each, all in one group). Per word and
@@ -462,7 +520,6 @@ __global__ __launch_bounds__(256) void cq4_gemv_kernel(Cq4View w, const float* _
     const uint32_t n = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (n >= w.N) return;  // whole wavefronts, after the only barrier
     const uint32_t K = w.K, words = K >> 3, wpg = gs >> 3;
-    const size_t pgb = gs >> 1;  // bytes of one row's group
     const float* arow[ROWS];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) arow[r] = ap + static_cast<size_t>(min(static_cast<uint32_t>(r), M - 1)) * K;
@@ -470,45 +527,82 @@ __global__ __launch_bounds__(256) void cq4_gemv_kernel(Cq4View w, const float* _
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) acc[r] = 0.0;
     for (uint32_t wi = lane; wi < words; wi += 64) {
-        const uint32_t g = wi / wpg, cw = wi % wpg;
-        uint32_t word;
         size_t ni;
-        if constexpr (INTER) {  // row n & 3 of panel n / 4: its word cw at byte 16 cw + 4 (n & 3)
-            const size_t panel = static_cast<size_t>(n >> 2) * ng + g;
-            word = *reinterpret_cast<const uint32_t*>(w.packed + panel * 4 * pgb + (n & 3) * 4 + 16 * cw);
-            ni = panel * 4 + (n & 3);
-        } else {
-            const size_t grp = static_cast<size_t>(n) * ng + g;
-            word = *reinterpret_cast<const uint32_t*>(w.packed + grp * pgb + 4 * cw);
-            ni = grp;
-        }
-        float cv[8];
-#pragma unroll
-        for (int t = 0; t < 8; ++t) cv[t] = lut[(word >> (4 * t)) & 0xFu];
-        const double norm = static_cast<double>(half_bits_to_float(w.norms[ni]));
-#pragma unroll
-        for (int r = 0; r < ROWS; ++r) {
-            const f32x4_t lo = *reinterpret_cast<const f32x4_t*>(arow[r] + 8 * wi);
-            const f32x4_t hi = *reinterpret_cast<const f32x4_t*>(arow[r] + 8 * wi + 4);
-            const float av[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            float sum = 0.0f;
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                // nibble t holds k = 8 cw + t (LSB) or 8 cw + (t >> 1) + 4 (t & 1) (interleaved)
-                const int kk = INTER ? (t >> 1) + 4 * (t & 1) : t;
-                sum = fmaf(av[kk], cv[t], sum);
-            }
-            acc[r] = fma(norm, static_cast<double>(sum), acc[r]);
-        }
+        const uint32_t word = cq4_gemv_word<INTER>(w, n, wi, wpg, ng, ni);
+        cq4_gemv_step<ROWS, INTER>(lut, word, w.norms[ni], arow, wi, acc);
     }
+    cq4_gemv_store<ROWS>(acc, c, w.N, M, n, lane);
+}
+
+// Rows x K values the fused GEMV transforms in LDS (two arrays of that many floats: 32 KiB).
+constexpr uint32_t kCq4FusedMaxValues = 4096;
+
+// The GEMV above with the Hadamard transform in the same launch (M <= 4, power-of-two group
+// size <= 256, M * K <= kCq4FusedMaxValues): every workgroup transforms all M rows into LDS with
+// the operations of cq4_transform_hadamard_kernel, in the same order (scale and left sign, the
+// butterflies of strides 1 .. gs / 2, then the permuted, normalized, right-signed values), so
+// its four wavefronts read exactly the values the two-launch form reads from memory, and run
+// its columns. Each lane's first index word and norm are loaded before the transform, so their
+// latency overlaps it; the call needs no workspace and one launch instead of two. Dynamic LDS:
+// 2 * M * K floats.
+template <int ROWS, bool INTER>
+__global__ __launch_bounds__(256) void cq4_gemv_fused_kernel(Cq4View w, const uint16_t* __restrict__ a,
+                                                            uint16_t* __restrict__ c, uint32_t M, uint32_t gs,
+                                                            uint32_t ng) {
+    extern __shared__ f32x4_t fused_lds[];
+    __shared__ float lut[16];
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t n = blockIdx.x * 4 + (tid >> 6);
+    const uint32_t K = w.K, words = K >> 3, wpg = gs >> 3, total = M * K;
+    float* xv = reinterpret_cast<float*>(fused_lds);  // scaled, signed, then transformed in place
+    float* xa = xv + total;                            // code-basis activations, row-major
+    if (tid < 16) lut[tid] = half_bits_to_float(w.codebook[tid]);
+    const bool live = n < w.N;  // uniform per wavefront; every wavefront takes part in the transform
+    uint32_t word0 = 0;
+    uint16_t norm0 = 0;
+    if (live && lane < words) {
+        size_t ni;
+        word0 = cq4_gemv_word<INTER>(w, n, lane, wpg, ng, ni);
+        norm0 = w.norms[ni];
+    }
+    for (uint32_t e = tid; e < total; e += 256) {
+        const uint32_t k = e % K;
+        const float sign = w.left_signs ? static_cast<float>(w.left_signs[k % gs]) : 1.0f;
+        xv[e] = half_bits_to_float(a[e]) * input_recip(w, k) * sign;
+    }
+    __syncthreads();
+    for (uint32_t h = 1; h < gs; h <<= 1) {  // butterflies over strides 1, 2, 4, ... (cactus_x86.cpp:56-66)
+        // butterfly t pairs j and j + h inside one block of 2h values, so never across a group
+        for (uint32_t t = tid; t < total / 2; t += 256) {
+            const uint32_t j = (t / h) * 2 * h + (t % h);
+            const float x = xv[j], y = xv[j + h];
+            xv[j] = x + y;
+            xv[j + h] = x - y;
+        }
+        __syncthreads();
+    }
+    const float inv = 1.0f / sqrtf(static_cast<float>(gs));
+    for (uint32_t e = tid; e < total; e += 256) {
+        const uint32_t j = e % gs;  // K % gs == 0: the position inside the element's group
+        const uint32_t src = w.permutation ? (w.permutation[j] & (gs - 1)) : j;
+        const float sign = w.right_signs ? static_cast<float>(w.right_signs[src]) : 1.0f;
+        xa[e] = xv[e - j + src] * inv * sign;
+    }
+    __syncthreads();
+    if (!live) return;
+    const float* arow[ROWS];
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r)
+    for (int r = 0; r < ROWS; ++r) arow[r] = xa + min(static_cast<uint32_t>(r), M - 1) * K;
+    double acc[ROWS];
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) acc[r] += __shfl_xor(acc[r], off);
-    if (lane == 0)
-#pragma unroll
-        for (int r = 0; r < ROWS; ++r)
-            if (static_cast<uint32_t>(r) < M) c[static_cast<size_t>(r) * w.N + n] = double_to_half_bits(acc[r]);
+    for (int r = 0; r < ROWS; ++r) acc[r] = 0.0;
+    if (lane < words) cq4_gemv_step<ROWS, INTER>(lut, word0, norm0, arow, lane, acc);
+    for (uint32_t wi = lane + 64; wi < words; wi += 64) {
+        size_t ni;
+        const uint32_t word = cq4_gemv_word<INTER>(w, n, wi, wpg, ng, ni);
+        cq4_gemv_step<ROWS, INTER>(lut, word, w.norms[ni], arow, wi, acc);
+    }
+    cq4_gemv_store<ROWS>(acc, c, w.N, M, n, lane);
 }
 
 // MFMA form for 4-bit LSB-packed indices (the packing of cactus_x86.cpp:24-43 with
@@ -1069,6 +1163,14 @@ bool cq4_uses_mfma(const Cq4View& w, uint32_t m) {
     return m >= kCq4MfmaMinRows && w.bits == 4 && !inter && gs % 32 == 0 && w.K % 64 == 0;
 }
 
+// Decode-sized Hadamard calls: transform and GEMV in one launch (cq4_gemv_fused_kernel).
+bool cq4_gemv_fused(const Cq4View& w, uint32_t m) {
+    const bool orth = (w.flags & kCq4FlagOrthogonal) != 0;
+    const uint32_t gs = w.group_size;
+    return !orth && m >= 1 && m <= 4 && w.bits == 4 && gs % 8 == 0 && gs <= 256 && (gs & (gs - 1)) == 0 &&
+           static_cast<uint64_t>(m) * w.K <= kCq4FusedMaxValues;
+}
+
 template <int ROWS>
 hipError_t launch_gemm(const Cq4View& w, const float* ap, uint16_t* c, uint32_t m, uint32_t gs, uint32_t ng,
                        hipStream_t stream) {
@@ -1086,6 +1188,7 @@ hipError_t launch_gemm(const Cq4View& w, const float* ap, uint16_t* c, uint32_t 
 }  // namespace
 
 size_t cq4_workspace_bytes(const Cq4View& w, uint32_t m) {
+    if (cq4_gemv_fused(w, m)) return 0;
     const size_t values = static_cast<size_t>(m) * w.K;  // K % 64 == 0 on the MFMA path: no padding
     return cq4_uses_mfma(w, m) ? values * 3 * sizeof(uint16_t) : values * sizeof(float);
 }
@@ -1094,6 +1197,20 @@ hipError_t launch_cq4_matmul(const Cq4View& w, const uint16_t* a, uint32_t m, ui
                              hipStream_t stream) {
     // The transform writes the code-basis activations as fp32 rows, or, for the MFMA GEMM, directly as
     // their bf16 limbs.
+    if (cq4_gemv_fused(w, m)) {
+        const dim3 grid((w.N + 3) / 4);
+        const size_t lds = 2 * sizeof(float) * m * w.K;
+        const bool inter = (w.flags & kCq4FlagInterleaved4Row) != 0;
+        const uint32_t gs = w.group_size, ng = w.num_groups;
+        if (m == 1) {
+            if (inter) hipLaunchKernelGGL((cq4_gemv_fused_kernel<1, true>), grid, dim3(256), lds, stream, w, a, c, m, gs, ng);
+            else hipLaunchKernelGGL((cq4_gemv_fused_kernel<1, false>), grid, dim3(256), lds, stream, w, a, c, m, gs, ng);
+        } else {
+            if (inter) hipLaunchKernelGGL((cq4_gemv_fused_kernel<4, true>), grid, dim3(256), lds, stream, w, a, c, m, gs, ng);
+            else hipLaunchKernelGGL((cq4_gemv_fused_kernel<4, false>), grid, dim3(256), lds, stream, w, a, c, m, gs, ng);
+        }
+        return hipGetLastError();
+    }
     const bool mfma = cq4_uses_mfma(w, m);
     float* ap = mfma ? nullptr : static_cast<float*>(workspace);
     uint16_t* xs = mfma ? static_cast<uint16_t*>(workspace) : nullptr;

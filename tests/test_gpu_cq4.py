@@ -75,7 +75,12 @@ CASES = [dict(bits=4, K=256, N=24, group_size=64, signs=True, perm=True, scale="
          dict(bits=4, K=96, N=8, group_size=96, orthogonal=True, m=2),
          dict(bits=3, K=64, N=8, group_size=64, orthogonal=True, scale="none", m=5),
          dict(bits=4, K=64, N=16, group_size=2, m=3),
-         dict(bits=4, K=16, N=4, group_size=1, m=2)]
+         dict(bits=4, K=16, N=4, group_size=1, m=2),
+         # M <= 4: transform and GEMV in one launch up to 4096 values of M x K, two launches beyond
+         dict(bits=4, K=256, N=20, group_size=64, interleaved=True, signs=True, perm=True, scale="scale", m=2),
+         dict(bits=4, K=2048, N=12, group_size=16, interleaved=True, m=2),
+         dict(bits=4, K=4096, N=12, group_size=128, interleaved=True, m=1),
+         dict(bits=4, K=2048, N=24, group_size=128, signs=True, perm=True, m=3)]
 
 
 @pytest.mark.parametrize("case", range(len(CASES)))
