@@ -260,10 +260,12 @@ typedef struct spaceslug_cq4_matrix {
 int spaceslug_cq4_matmul(const spaceslug_cq4_matrix* w, const uint16_t* a, uint32_t m, uint16_t* c);
 
 /* Device-pointer, stream-ordered variant: every array of `w` (the struct itself
- * is host memory) and a, c are device pointers. The code-basis activations (M * K
- * floats) live in the library-owned device workspace of spaceslug_q4gemm_device,
- * ordered the same way across streams; under stream capture the call returns
- * SPACESLUG_ERR_UNSUPPORTED. */
+ * is host memory) and a, c are device pointers. The code-basis activations live in
+ * the library-owned device workspace of spaceslug_q4gemm_device, ordered the same
+ * way across streams; under stream capture such a call returns
+ * SPACESLUG_ERR_UNSUPPORTED. Decode calls (Hadamard basis, 4-bit indices, M <= 4,
+ * group size a multiple of 8, M * K <= 4096) run as one launch without the
+ * workspace and may be captured. */
 int spaceslug_cq4_matmul_device(const spaceslug_cq4_matrix* w, const uint16_t* d_a, uint32_t m, uint16_t* d_c,
                                 void* stream);
 

@@ -678,9 +678,14 @@ int spaceslug_cq4_matmul_device(const spaceslug_cq4_matrix* w, const uint16_t* d
     try {
         DeviceState& dev = current_device();
         const hipStream_t st = static_cast<hipStream_t>(stream);
+        const size_t ws_bytes = spaceslug::cq4_workspace_bytes(v, m);
+        if (ws_bytes == 0) {  // one launch, no workspace (decode sizes): capturable
+            check(spaceslug::launch_cq4_matmul(v, d_a, m, d_c, nullptr, st), "cq4 launch");
+            return ok();
+        }
         if (const int rc = refuse_capture(st, "spaceslug_cq4_matmul_device")) return rc;
         std::lock_guard<std::mutex> lock(g_device_mutex);
-        void* ws = device_workspace(dev, spaceslug::cq4_workspace_bytes(v, m));
+        void* ws = device_workspace(dev, ws_bytes);
         if (!dev.ws_done) check(hipEventCreateWithFlags(&dev.ws_done, hipEventDisableTiming), "hipEventCreateWithFlags");
         if (dev.ws_used && dev.ws_stream != st) check(hipStreamWaitEvent(st, dev.ws_done, 0), "hipStreamWaitEvent");
         check(spaceslug::launch_cq4_matmul(v, d_a, m, d_c, ws, st), "cq4 launch");

@@ -210,3 +210,57 @@ def test_device_calls_in_a_row(session, gpu):
         assert np.array_equal(dev, run(session, W, A, M)), call
         ok, _ = within_fp16_rounding(dev, cq4.matmul(W, A, M))
         assert ok, call
+
+
+def test_decode_call_in_a_hip_graph(session, gpu):
+    """A decode call (1 x 512 x 512, the reference benchmark's decode shape: one launch, no workspace)
+    captured once in a HIP graph and replayed with new activations: every replay equals the eager call
+    bit for bit and the oracle to the fp16 bar. A call that needs the workspace (M = 64) is refused
+    under capture, and the capture still ends cleanly."""
+    import ctypes
+
+    import torch
+
+    note("cq4 decode call in a HIP graph")
+    rng = np.random.default_rng(777)
+    W = cq4.random_matrix(rng, bits=4, K=512, N=512, group_size=128, signs=True, perm=True, scale="scale")
+    keep = {}
+    s = device_struct(W, keep)
+    a_t = torch.zeros((1, W.K), dtype=torch.int16, device="cuda:0")
+    c_t = torch.zeros((1, W.N), dtype=torch.int16, device="cuda:0")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        session.cq4_matmul_device(s, a_t.data_ptr(), 1, c_t.data_ptr(), side.cuda_stream)  # warm-up
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        session.cq4_matmul_device(s, a_t.data_ptr(), 1, c_t.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        A = cq4.f16(rng.uniform(-1, 1, (1, W.K)))
+        a_t.copy_(torch.from_numpy(A.view(np.int16).copy()).to("cuda:0"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = c_t.cpu().numpy().view(np.uint16).copy()
+        eager = run_device(session, s, a_t.data_ptr(), 1, W.N)
+        assert np.array_equal(got, eager), f"replay {rep} differs from the eager call"
+        ok, _ = within_fp16_rounding(got, cq4.matmul(W, A, 1))
+        assert ok, rep
+
+    M = 64
+    a64 = torch.zeros((M, W.K), dtype=torch.int16, device="cuda:0")
+    c64 = torch.zeros((M, W.N), dtype=torch.int16, device="cuda:0")
+    lib = session._native()
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2, stream=side):
+        c64.add_(1)
+        rc = lib.spaceslug_cq4_matmul_device(ctypes.addressof(s), ctypes.c_void_p(a64.data_ptr()), M,
+                                             ctypes.c_void_p(c64.data_ptr()), ctypes.c_void_p(side.cuda_stream))
+    assert rc == -4
+    assert b"workspace" in lib.spaceslug_last_error()
+    g2.replay()
+    torch.cuda.synchronize()
+    assert torch.all(c64 == 1)
