@@ -677,6 +677,316 @@ __global__ __launch_bounds__(512) void q4_gemm_wide_kernel(const uint16_t* xs, c
     }
 }
 
+// Mid-size tiles for M > 32 when the 128 x 128 grid would leave CUs idle and need a K-split plus
+// a reduction launch (the reference benchmark's M = N = K = 1024: 64 wide tiles): 64 x 64 outputs
+// per workgroup of 8 wavefronts over the whole of K, no partials in memory. x comes as bf16 limbs
+// laid out [M][K/64][3][64] (x_limb_rows_kernel), and the design is that of the pipelined CQ4
+// kernel (cq4.hip) with one weight limb:
+//   - wavefront w owns the 32 x 32 output tile (rows 32 (w & 1), columns 32 ((w >> 1) & 1)) for
+//     the 32-value group (w >> 2) of every 64-value stage, so the two wavefronts of a SIMD split K
+//     by groups; per stage a wavefront runs one chain of 6 v_mfma_f32_32x32x16_bf16 (limbs 2, 1, 0,
+//     smallest first, each over the group's two 16-value halves: the order of the wide kernel) and
+//     folds the previous stage's group sums into float64 between them (acc += s * P, 32 operations);
+//     the two halves of K are added in double through LDS at the end, and the sums multiplied by
+//     16 (the weights enter as v / 16) before the single fp32 store;
+//   - every operand reaches LDS by global_load_lds: the x limbs four stages deep (wavefront w
+//     copies the 8-row block w of each limb, rows paired and 16-byte chunks swizzled), the packed
+//     weights by stage pairs (each thread copies the two words it decodes, one per stage), the
+//     tile's scales (all groups) once before the loop;
+//   - one stage ahead of its use each thread decodes its word through the byte table into the B
+//     layout of pipe_b_slot, conflict-free for the writes and the MFMA reads;
+//   - iteration t copies stage t + 4 into slot t % 4 and on even t the stage pair t + 4, t + 5,
+//     then runs stage t's chain with, between its MFMAs, stage t - 1's fold, the operand reads of
+//     stage t + 1 and the decode of stage t + 2, and passes one barrier. Past the last stage the
+//     copied stage is clamped, so every wavefront issues the same copies per iteration and
+//     `s_waitcnt vmcnt(8)` leaves exactly the two younger stages and one pair in flight.
+constexpr int kMidTile = 64;
+constexpr int kMidStages = 4;
+constexpr int kMidWaves = 8;
+constexpr int kMidGroupsMax = 128;  // scale groups per column held in LDS (K <= 4096)
+
+struct MidLds {
+    // byte b of packed weights -> the bf16 values v / 16 of its low and high nibbles (low and high
+    // half); first, so that ds_read's 16-bit offset field reaches it from a byte-scaled address
+    uint32_t lut[256];
+    u32x4 a[kMidStages][kLimbs][8][64];      // stage, limb, 8-row block, 16-byte chunk (row pairs)
+    uint32_t braw[2][kMidWaves][2][64];      // stage-pair slot, wavefront, stage of the pair, thread
+    u32x4 b[2][2][2][2][64];                 // stage parity, group of the stage, 32-column tile, half, slot
+    float s[kMidTile * kMidGroupsMax + 64];  // tile column, group (as in the array); copy slack
+};
+static_assert(sizeof(MidLds) <= 160 * 1024, "LDS budget");
+
+// x (fp32, M x K, K % 64 == 0) -> its bf16 limbs laid out [M][K/64][3][64] (row, 64-value stage,
+// limb, value) for q4_gemm_mid_kernel: one thread per 8 values, two 16-byte loads and three 16-byte
+// stores (8 consecutive threads write one limb's 128-byte run of a stage).
+__global__ __launch_bounds__(256) void x_limb_rows_kernel(const float* __restrict__ x, uint16_t* __restrict__ xs,
+                                                         int M, int K) {
+    const size_t e = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;  // 8-value unit
+    const size_t per_row = static_cast<size_t>(K >> 3);
+    if (e >= static_cast<size_t>(M) * per_row) return;
+    const size_t row = e / per_row, c = e % per_row;
+    const float* src = x + row * K + 8 * c;
+    const f32x4 lo = *reinterpret_cast<const f32x4*>(src);
+    const f32x4 hi = *reinterpret_cast<const f32x4*>(src + 4);
+    u32x4 limb[kLimbs];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        uint32_t l0[kLimbs], l1[kLimbs];
+        split_bf16_limbs(t < 2 ? lo[2 * t] : hi[2 * t - 4], l0);
+        split_bf16_limbs(t < 2 ? lo[2 * t + 1] : hi[2 * t - 3], l1);
+#pragma unroll
+        for (int li = 0; li < kLimbs; ++li) limb[li][t] = l0[li] | (l1[li] << 16);
+    }
+    uint16_t* dst = xs + (row * (K >> 6) + (c >> 3)) * (kLimbs * 64) + 8 * (c & 7);
+#pragma unroll
+    for (int li = 0; li < kLimbs; ++li) *reinterpret_cast<u32x4*>(dst + li * 64) = limb[li];
+}
+
+// x, wq and ws are not __restrict__ for the reason given at q4_gemm_mfma_kernel.
+__global__ __launch_bounds__(64 * kMidWaves) void q4_gemm_mid_kernel(const uint16_t* xs, const uint32_t* wq,
+                                                                    const float* ws, float* __restrict__ y, int M,
+                                                                    int N, int K, int tiles_m) {
+    __shared__ MidLds lds;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wid & 1, wn = (wid >> 1) & 1, ku = wid >> 2;
+    const int col32 = lane & 31, half = lane >> 5;
+    const int T = K / 64;
+    const int G = K / 32;
+    const int mt0 = static_cast<int>(blockIdx.x % tiles_m) * kMidTile;
+    const int nt0 = static_cast<int>(blockIdx.x / tiles_m) * kMidTile;
+
+    // x-limb copy of this wavefront: 8-row block wid (row pairs 4 wid .. 4 wid + 3); lane l copies
+    // chunk (l % 8) ^ (pair % 8) of its row, so that chunk c of a row sits at slot c ^ (pair % 8).
+    const uint16_t* asrc;
+    {
+        const int pair = 4 * wid + (lane >> 4);
+        const int row_t = 2 * pair + ((lane >> 3) & 1);
+        asrc = xs + static_cast<size_t>(min(mt0 + row_t, M - 1)) * T * (kLimbs * 64) + 8 * ((lane & 7) ^ (pair & 7));
+    }
+    // Packed word this thread decodes: group bu of the stage, tile column bc, word bw of the group.
+    const int bc = 8 * wid + (lane >> 3), bu = (lane >> 2) & 1, bw = lane & 3;
+    const int bdst = pipe_b_slot((bc & 31) + 32 * (bw & 1), bw >> 1, bu);
+    const char* bsrc = reinterpret_cast<const char*>(wq) + static_cast<size_t>(min(nt0 + bc, N - 1)) * (K >> 1) +
+                       4 * (lane & 7);
+    // This lane's A operand: row 32 wm + (lane & 31), chunk 4 ku + 2 h + (lane >> 5) of a stage for half h.
+    const int ar = 32 * wm + col32;
+    const int apr = ar >> 1;
+    const int aidx0 = apr * 16 + 8 * (ar & 1) + ((4 * ku + half) ^ (apr & 7));
+    const int aidx1 = apr * 16 + 8 * (ar & 1) + ((4 * ku + 2 + half) ^ (apr & 7));
+    const int bsrc0 = pipe_b_slot(lane, 0, ku), bsrc1 = pipe_b_slot(lane, 1, ku);
+
+    // Stage t's limbs into stage slot st (past the last stage, t is clamped and st is not).
+    auto issue = [&](int t, int st) {
+#pragma unroll
+        for (int li = 0; li < kLimbs; ++li)
+            __builtin_amdgcn_global_load_lds(asrc + static_cast<size_t>(t) * (kLimbs * 64) + li * 64,
+                                             &lds.a[st][li][wid][0], 16, 0, 0);
+    };
+    // Packed weights of stages 2 j and 2 j + 1 into slot `slot`, one 4-byte copy per stage (clamped
+    // to the last stage past the end of the column).
+    auto issue_b = [&](int j, int slot) {
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc)
+            __builtin_amdgcn_global_load_lds(bsrc + min(32 * (2 * j + cc), (K >> 1) - 32), &lds.braw[slot][wid][cc][0], 4,
+                                             0, 0);
+    };
+    auto decode_word = [&](int t) { return lds.braw[(t >> 1) & 1][wid][t & 1][lane]; };
+    auto decode_lookup = [&](uint32_t wd, u32x4& v) {  // one table entry per byte (two values)
+        typedef __attribute__((address_space(3))) const volatile uint32_t lds_word;
+        lds_word* lut = (lds_word*)(&lds.lut[0]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = lut[(wd >> (8 * j)) & 0xFFu];
+    };
+    auto decode_write = [&](int t, const u32x4& v) { lds.b[t & 1][bu][bc >> 5][bw >> 1][bdst] = v; };
+    auto barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+
+    // The tile's scales (64 columns of G values, contiguous in the array), then stages 0 .. 3 and
+    // pairs 0 and 1; stages 2 and 3 and pair 1 stay in flight while stages 0 and 1 are decoded and
+    // read: `s_waitcnt vmcnt(8)` leaves exactly their 3 + 3 + 2 copies outstanding.
+    {
+        const char* ssrc = reinterpret_cast<const char*>(ws) + static_cast<size_t>(nt0) * G * 4;
+        const int units = kMidTile * G;  // 4-byte units
+        const size_t last = static_cast<size_t>(N - nt0) * G * 4 - 4;
+        for (int b = wid; 64 * b < units; b += kMidWaves)  // uniform
+            __builtin_amdgcn_global_load_lds(ssrc + min(static_cast<size_t>(4 * (64 * b + lane)), last),
+                                             reinterpret_cast<char*>(lds.s) + 256 * b, 4, 0, 0);
+    }
+    const int jmax = (T - 1) / 2;  // the last stage pair
+    issue(0, 0);
+    issue_b(0, 0);
+    issue(min(1, T - 1), 1);
+    issue(min(2, T - 1), 2);
+    issue_b(min(1, jmax), 1);
+    issue(min(3, T - 1), 3);
+    if (tid < 256) {  // the byte table, the same conversions as nibbles_bf16_16th
+        const uint32_t lo = __float_as_uint(__builtin_amdgcn_cvt_off_f32_i4(tid));
+        const uint32_t hi = __float_as_uint(__builtin_amdgcn_cvt_off_f32_i4(tid >> 4));
+        lds.lut[tid] = (lo >> 16) | (hi & 0xFFFF0000u);
+    }
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    barrier();  // scales and table visible, every wavefront's stages 0 and 1 and pair 0 copied
+    {
+        u32x4 v0, v1;
+        const uint32_t w0 = decode_word(0), w1 = decode_word(1);
+        decode_lookup(w0, v0);
+        decode_lookup(w1, v1);
+        decode_write(0, v0);
+        decode_write(1, v1);  // past the last stage: an unread buffer from a clamped copy
+    }
+    barrier();
+
+    struct Operands {
+        bf16x8 a[kLimbs][2], b[2];
+    };
+    Operands ops[2];
+    // Operand reads of stage t in the order the chain uses them: limb 2, weights, limb 1, limb 0.
+    auto read_part = [&](Operands& o, int t, int part) {
+        const int sidx = t & (kMidStages - 1), par = t & 1;
+        if (part == 1) {
+            o.b[0] = __builtin_bit_cast(bf16x8, lds.b[par][ku][wn][0][bsrc0]);
+            o.b[1] = __builtin_bit_cast(bf16x8, lds.b[par][ku][wn][1][bsrc1]);
+        } else {
+            const int li = part == 0 ? 2 : (part == 2 ? 1 : 0);
+            o.a[li][0] = __builtin_bit_cast(bf16x8, (&lds.a[sidx][li][0][0])[aidx0]);
+            o.a[li][1] = __builtin_bit_cast(bf16x8, (&lds.a[sidx][li][0][0])[aidx1]);
+        }
+    };
+#pragma unroll
+    for (int part = 0; part < 4; ++part) read_part(ops[0], 0, part);
+    barrier();  // stage 0's slot is read before iteration 0 copies into it
+
+    f32x16 zero16;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) zero16[v] = 0.0f;
+    double acc[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.0;
+    struct Stage {
+        f32x16 p;
+        double s;
+    };
+    Stage st_buf[2];
+    st_buf[1].p = zero16;  // iteration 0 folds these zeros
+    st_buf[1].s = 0.0;
+    // fold operation f (0 .. 31) of a stage: per result a conversion, then (one result later) a
+    // float64 FMA acc += s * P
+    double pd[2];
+    auto fold_op = [&](const Stage& r, int f) {
+        if (f == 0) {
+            pd[0] = static_cast<double>(r.p[0]);
+        } else if (f == 31) {
+            acc[15] = fma(r.s, pd[1], acc[15]);
+        } else if (f & 1) {
+            const int o = (f + 1) >> 1;  // 1 .. 15
+            pd[o & 1] = static_cast<double>(r.p[o]);
+        } else {
+            const int o = (f - 2) >> 1;  // 0 .. 14
+            acc[o] = fma(r.s, pd[o & 1], acc[o]);
+        }
+    };
+    const float* srow = lds.s + (32 * wn + col32) * G + ku;  // this lane's column, group ku of stage 0
+
+    for (int t0 = 0; t0 < T; t0 += 2) {
+        static_for<2>([&](auto uc) {
+            constexpr int u = decltype(uc)::value;
+            const int t = t0 + u;
+            if (t < T) {  // uniform
+                Stage& cur = st_buf[u];
+                const Stage& old = st_buf[u ^ 1];
+                const Operands& op = ops[u];
+                Operands& nxt = ops[u ^ 1];
+                issue(min(t + 4, T - 1), t & (kMidStages - 1));
+                if constexpr (u == 0) issue_b(min(t / 2 + 2, jmax), (t / 2) & 1);  // t is even
+                uint32_t wd = 0;
+                u32x4 dec;
+                float sraw = 0.0f;
+                static_for<6>([&](auto ic) {
+                    constexpr int i = decltype(ic)::value;
+                    constexpr int li = 2 - (i >> 1), h = i & 1;
+                    cur.p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op.a[li][h], op.b[h], i == 0 ? zero16 : cur.p, 0,
+                                                                    0, 0);
+                    __builtin_amdgcn_sched_barrier(0);  // the MFMA first: a wait below stalls only the rest
+                    constexpr int f0 = i < 2 ? 6 * i : 12 + 5 * (i - 2);
+                    constexpr int f1 = i < 2 ? f0 + 6 : f0 + 5;
+                    static_for<f1 - f0>([&](auto fc) { fold_op(old, f0 + decltype(fc)::value); });
+                    if constexpr (i == 0) {
+                        // this wavefront's copies of stage t + 2 and of its pair; after them come stages
+                        // t + 3, t + 4 and one pair (3 + 3 + 2 copies)
+                        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+                        wd = decode_word(t + 2);
+                        sraw = srow[2 * t];
+                    }
+                    if constexpr (i == 1) decode_lookup(wd, dec);
+                    if constexpr (i == 5) decode_write(t + 2, dec);  // past the last stage: an unread buffer
+                    if constexpr (i >= 2) read_part(nxt, t + 1, i - 2);  // past the last stage: unused
+                    if constexpr (i == 3) cur.s = static_cast<double>(sraw);
+                    __builtin_amdgcn_sched_barrier(0);
+                });
+                barrier();
+            }
+        });
+    }
+    if (T & 1) {  // uniform: the last stage's sums are in st_buf[(T - 1) % 2]
+#pragma unroll
+        for (int f = 0; f < 32; ++f) fold_op(st_buf[0], f);
+    } else {
+#pragma unroll
+        for (int f = 0; f < 32; ++f) fold_op(st_buf[1], f);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped copies past the last stage
+    // The two halves of K of each tile, added in double: the wavefront of group u finishes results
+    // 8 u .. 8 u + 7 of its tile and hands the other eight to its partner through LDS; the fp32 tile
+    // is then assembled in LDS and stored as 32-byte row pieces.
+    double* red = reinterpret_cast<double*>(&lds.a[0][0][0][0]);  // [4 tiles][16 results][64 lanes]
+    float* tile = reinterpret_cast<float*>(&lds.b[0][0][0][0][0]);  // [64 rows][64 columns]
+    static_assert(sizeof(lds.b) >= sizeof(float) * kMidTile * kMidTile, "the output tile fits");
+    auto hand_over = [&](auto mine_c) {
+        constexpr int other = 8 - decltype(mine_c)::value;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) red[((wid & 3) * 16 + other + v) * 64 + lane] = acc[other + v];
+    };
+    auto finish = [&](auto mine_c) {
+        constexpr int mine = decltype(mine_c)::value;
+#pragma unroll
+        for (int v = mine; v < mine + 8; ++v) {
+            const int row = 32 * wm + 8 * (v >> 2) + 4 * half + (v & 3);
+            const double s = acc[v] + red[((wid & 3) * 16 + v) * 64 + lane];
+            tile[row * kMidTile + 32 * wn + col32] = static_cast<float>(s * 16.0);
+        }
+    };
+    __syncthreads();  // every wavefront is past its last read of lds.a and lds.b, and every copy has landed
+    if (ku == 0)
+        hand_over(std::integral_constant<int, 0>{});
+    else
+        hand_over(std::integral_constant<int, 8>{});
+    __syncthreads();
+    if (ku == 0)
+        finish(std::integral_constant<int, 0>{});
+    else
+        finish(std::integral_constant<int, 8>{});
+    __syncthreads();
+    {
+        const int rl = tid >> 3, c8 = 8 * (tid & 7);  // tile row, first of 8 columns
+        const int row = mt0 + rl, col = nt0 + c8;
+        const f32x4 v0 = *reinterpret_cast<const f32x4*>(&tile[rl * kMidTile + c8]);
+        const f32x4 v1 = *reinterpret_cast<const f32x4*>(&tile[rl * kMidTile + c8 + 4]);
+        const bool vec = N % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;  // uniform
+        if (row < M) {
+            float* dst = y + static_cast<size_t>(row) * N + col;
+            if (vec && col + 8 <= N) {
+                *reinterpret_cast<f32x4*>(dst) = v0;
+                *reinterpret_cast<f32x4*>(dst + 4) = v1;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (col + e < N) dst[e] = e < 4 ? v0[e] : v1[e - 4];
+            }
+        }
+    }
+}
+
 // LoRA pre-pass on the MFMA: tpart[z][m][r] = sum over the kLoraGroupsPerBlock groups
 // of split z of x[m][k] * la[k][r] (la is K x R row-major). One workgroup of 4
 // wavefronts per 16 x 16 tile of (rows, ranks) and split; each wavefront takes
@@ -1044,6 +1354,14 @@ Q4Plan plan_q4gemm(const DeviceInfo& dev, uint32_t m, uint32_t n, uint32_t k, ui
     const int per_split = (groups + splits - 1) / splits;
     splits = (groups + per_split - 1) / per_split;
     plan.splits = splits;
+    const size_t mid_tiles = static_cast<size_t>((m + kMidTile - 1) / kMidTile) * ((n + kMidTile - 1) / kMidTile);
+    if (plan.kind == Q4Plan::kWide && splits > 1 && rank == 0 && k % 64 == 0 && groups <= kMidGroupsMax &&
+        mid_tiles <= static_cast<size_t>(dev.cu_count)) {
+        plan.kind = Q4Plan::kMid;  // whole K per 64 x 64 tile: no partials, no reduction launch
+        plan.splits = 1;
+        plan.workspace_bytes = align_up(static_cast<size_t>(m) * k * kLimbs * sizeof(uint16_t));  // x limbs
+        return plan;
+    }
     size_t bytes = lora_bytes;
     if (plan.kind == Q4Plan::kWide) bytes += align_up(split_x_bf16_bytes(m, k));  // x limbs
     if (splits > 1) bytes += align_up(static_cast<size_t>(splits) * m * n * sizeof(float));
@@ -1056,6 +1374,20 @@ hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float*
                          uint32_t n, uint32_t k, const float* la, const float* lb, uint32_t rank,
                          float lora_scale, void* workspace, hipStream_t stream) {
     if (plan.kind == Q4Plan::kGemv) return launch_gemv(dev, x, w_packed, w_scales, y, m, n, k, stream);
+    if (plan.kind == Q4Plan::kMid) {
+        uint16_t* xs = static_cast<uint16_t*>(workspace);
+        const size_t units = static_cast<size_t>(m) * (k / 8);
+        hipLaunchKernelGGL(x_limb_rows_kernel, dim3(static_cast<unsigned>((units + 255) / 256)), dim3(256), 0, stream,
+                           x, xs, static_cast<int>(m), static_cast<int>(k));
+        const hipError_t pe = hipGetLastError();
+        if (pe != hipSuccess) return pe;
+        const int tiles_m = static_cast<int>((m + kMidTile - 1) / kMidTile);
+        const int tiles_n = static_cast<int>((n + kMidTile - 1) / kMidTile);
+        hipLaunchKernelGGL(q4_gemm_mid_kernel, dim3(tiles_m * tiles_n), dim3(64 * kMidWaves), 0, stream, xs,
+                           reinterpret_cast<const uint32_t*>(w_packed), w_scales, y, static_cast<int>(m),
+                           static_cast<int>(n), static_cast<int>(k), tiles_m);
+        return hipGetLastError();
+    }
 
     char* wsp = static_cast<char*>(workspace);
     float* partial = nullptr;

@@ -22,8 +22,10 @@ constexpr int kGemvMaxRows = 4;
 // Launch shape chosen by plan_q4gemm for one call.
 struct Q4Plan {
     // kGemv: decode GEMV (m <= 4, no LoRA); kSkinny: m <= 32 with k % 128 == 0, K split
-    // inside the workgroup; kSkinnySplitK: other m <= 32; kWide: m > 32.
-    enum Kind { kGemv, kSkinny, kSkinnySplitK, kWide } kind;
+    // inside the workgroup; kSkinnySplitK: other m <= 32; kWide: m > 32; kMid: m > 32 without
+    // LoRA whose 128 x 128 grid would need a K-split while its 64 x 64 grid fits the CUs once
+    // (k % 64 == 0, k <= 4096).
+    enum Kind { kGemv, kSkinny, kSkinnySplitK, kWide, kMid } kind;
     int splits;              // K-splits of the MFMA kernel (1 = write y directly)
     size_t workspace_bytes;  // device scratch the call needs (split partials, LoRA T partials and T, x limbs)
     int t_splits;            // K-splits of the LoRA pre-pass T = x * lora_a (0 without LoRA)

@@ -126,6 +126,19 @@ def test_mfma_shapes(session, oracle, gpu, m, n, k):
     check(oracle, got, oracle.q4gemm_packed(c.x, c.packed, c.scales, threads=threads()), label=f"mfma {m}x{n}x{k}")
 
 
+@pytest.mark.parametrize("m,n,k", [(33, 65, 320), (100, 301, 512), (40, 100, 4096), (96, 2000, 256),
+                                   (250, 640, 704), (1024, 1024, 1024)])
+def test_mid_tile_shapes(session, oracle, gpu, m, n, k):
+    """Shapes whose 128 x 128 grid would need a K-split and whose 64 x 64 grid fits the CUs once: the
+    mid-size kernel over the whole of K (odd stage count at K = 320 and 704, the most scale groups
+    held in LDS at K = 4096, ragged rows and columns, a column count that is not a multiple of 4,
+    the reference benchmark's 1024^3)."""
+    note(f"mid m={m} n={n} k={k}")
+    c = make_case(m, n, k)
+    got = session.q4gemm_values(c.x, c.packed, c.scales, m, n, k)
+    check(oracle, got, oracle.q4gemm_packed(c.x, c.packed, c.scales, threads=threads()), label=f"mid {m}x{n}x{k}")
+
+
 def test_wide_one_split_many_groups(session, oracle, gpu):
     """Wide kernel with one K split (135 tiles of 128 x 128 fill the 256 CUs at two wavefronts per
     SIMD without splitting K) and an odd group count (33): every workgroup runs the whole K loop,
@@ -465,13 +478,14 @@ def test_device_entry_on_side_stream(session, oracle, gpu):
     check(oracle, y.cpu().numpy(), oracle.q4gemm_packed(c.x, c.packed, c.scales), label="side stream")
 
 
-def test_split_k_calls_on_two_streams(session, oracle, gpu):
-    """Two K-split calls (they share the library's device workspace) enqueued back to back on two
-    streams, several rounds: the second stream must wait for the first's partial sums to be consumed."""
+@pytest.mark.parametrize("m,n,k", [(64, 1024, 8192), (64, 1024, 4096)])
+def test_split_k_calls_on_two_streams(session, oracle, gpu, m, n, k):
+    """Two calls that share the library's device workspace enqueued back to back on two streams, several
+    rounds: the second stream must wait for the first's workspace to be consumed. At K = 8192 the wide
+    kernel splits K 32 ways into partial sums; at K = 4096 the mid-size kernel reads x limbs from it."""
     import torch
 
-    m, n, k = 64, 1024, 4096  # one row of 128x128 tiles: K is split 16 ways into the workspace
-    note("split-K workspace shared by two streams")
+    note(f"workspace shared by two streams {m}x{n}x{k}")
     cases = [make_case(m, n, k, seed_a=0x100 + i, seed_b=0x200 + i, seed_s=0x300 + i) for i in range(2)]
     want = [oracle.q4gemm_packed(c.x, c.packed, c.scales, threads=threads()) for c in cases]
     streams = [torch.cuda.Stream(), torch.cuda.Stream()]
