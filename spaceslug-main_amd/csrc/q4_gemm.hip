@@ -718,13 +718,26 @@ static_assert(sizeof(MidLds) <= 160 * 1024, "LDS budget");
 
 // x (fp32, M x K, K % 64 == 0) -> its bf16 limbs laid out [M][K/64][3][64] (row, 64-value stage,
 // limb, value) for q4_gemm_mid_kernel: one thread per 8 values, two 16-byte loads and three 16-byte
-// stores (8 consecutive threads write one limb's 128-byte run of a stage).
+// stores (8 consecutive threads write one limb's 128-byte run of a stage). With xcd_rows set (the
+// GEMM's 64-row tiles a multiple of 8), workgroup b works on the rows of tiles t with t % 8 == b % 8:
+// workgroups run on XCD b % 8 and the GEMM reads row tile t on XCD t % 8, so each row's limbs are
+// written through the L2 that later serves them.
 __global__ __launch_bounds__(256) void x_limb_rows_kernel(const float* __restrict__ x, uint16_t* __restrict__ xs,
-                                                         int M, int K) {
-    const size_t e = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;  // 8-value unit
+                                                         int M, int K, bool xcd_rows) {
     const size_t per_row = static_cast<size_t>(K >> 3);
-    if (e >= static_cast<size_t>(M) * per_row) return;
-    const size_t row = e / per_row, c = e % per_row;
+    size_t row, c;
+    if (xcd_rows) {
+        const size_t u = static_cast<size_t>(blockIdx.x / 8) * 256 + threadIdx.x;  // unit in XCD lane b % 8
+        const size_t lr = u / per_row;                                             // row of that lane
+        row = (blockIdx.x % 8 + 8 * (lr / kMidTile)) * kMidTile + lr % kMidTile;
+        c = u - lr * per_row;
+        if (row >= static_cast<size_t>(M)) return;
+    } else {
+        const size_t e = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;  // 8-value unit
+        if (e >= static_cast<size_t>(M) * per_row) return;
+        row = e / per_row;
+        c = e % per_row;
+    }
     const float* src = x + row * K + 8 * c;
     const f32x4 lo = *reinterpret_cast<const f32x4*>(src);
     const f32x4 hi = *reinterpret_cast<const f32x4*>(src + 4);
@@ -1376,12 +1389,15 @@ hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float*
     if (plan.kind == Q4Plan::kGemv) return launch_gemv(dev, x, w_packed, w_scales, y, m, n, k, stream);
     if (plan.kind == Q4Plan::kMid) {
         uint16_t* xs = static_cast<uint16_t*>(workspace);
-        const size_t units = static_cast<size_t>(m) * (k / 8);
-        hipLaunchKernelGGL(x_limb_rows_kernel, dim3(static_cast<unsigned>((units + 255) / 256)), dim3(256), 0, stream,
-                           x, xs, static_cast<int>(m), static_cast<int>(k));
+        const int tiles_m = static_cast<int>((m + kMidTile - 1) / kMidTile);
+        const bool xcd_rows = tiles_m % 8 == 0;  // the GEMM then reads row tile t on XCD t % 8
+        // XCD lane b % 8 holds tiles_m / 8 row tiles of 64 rows (the last may be partial)
+        const size_t units = xcd_rows ? static_cast<size_t>(tiles_m / 8) * kMidTile * (k / 8) : static_cast<size_t>(m) * (k / 8);
+        const size_t blocks = xcd_rows ? 8 * ((units + 255) / 256) : (units + 255) / 256;
+        hipLaunchKernelGGL(x_limb_rows_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, x, xs,
+                           static_cast<int>(m), static_cast<int>(k), xcd_rows);
         const hipError_t pe = hipGetLastError();
         if (pe != hipSuccess) return pe;
-        const int tiles_m = static_cast<int>((m + kMidTile - 1) / kMidTile);
         const int tiles_n = static_cast<int>((n + kMidTile - 1) / kMidTile);
         hipLaunchKernelGGL(q4_gemm_mid_kernel, dim3(tiles_m * tiles_n), dim3(64 * kMidWaves), 0, stream, xs,
                            reinterpret_cast<const uint32_t*>(w_packed), w_scales, y, static_cast<int>(m),
