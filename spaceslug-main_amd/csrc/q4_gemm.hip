@@ -1,13 +1,14 @@
 // MFMA int4 GEMM for 5+ rows (prefill, small-batch decode, LoRA projections).
-// Three kernels: q4_gemm_wide_kernel for M > 32, q4_gemm_skinny_kernel for
+// Four kernels: q4_gemm_wide_kernel for M > 32, q4_gemm_mid_kernel for M > 32
+// shapes whose wide grid would need a K-split, q4_gemm_skinny_kernel for
 // M <= 32 with K % 128 == 0 and q4_gemm_mfma_kernel (K-split) for the other
 // M <= 32 shapes, each described at its definition.
 //
 // Replaces q4gemm.comp:61-175 (64x64 tile, LDS-staged dequantised B, 4x4 FMA
 // micro-tile per thread) with a CDNA4 design on the matrix cores: the two
-// small-M kernels on v_mfma_f32_16x16x4_f32, the wide kernel on
+// small-M kernels on v_mfma_f32_16x16x4_f32, the wide and mid-size kernels on
 // v_mfma_f32_32x32x16_bf16 with x split exactly into three bf16 limbs.
-// Common to all three:
+// Common to all of them:
 //   - per 32-value scale group, each lane feeds the MFMA K slots with 8
 //     consecutive K values, so its B operands for one column are the 8 nibbles
 //     of ONE 32-bit word of the packed column and its A operands are 8
@@ -22,7 +23,8 @@
 //   - large grids are XCD-aware: workgroup ids are remapped so each of the 8
 //     XCDs (one L2 each) walks a contiguous band of output tiles, sharing A
 //     rows and weight columns within its L2;
-//   - when the grid is too small to fill 256 CUs, K is split across
+//   - when the grid is too small to fill 256 CUs, the mid-size kernel's 64 x 64
+//     tiles take the shape if they fill the CUs once, else K is split across
 //     blockIdx.y and a second kernel sums the partials in a fixed order.
 // LoRA: the preparation launch that splits x into limbs also computes T = x * la on
 // the MFMA as a few K-split partials (one per 1024 values of K), and the GEMM
