@@ -695,7 +695,7 @@ __global__ __launch_bounds__(512) void q4_gemm_wide_kernel(const uint16_t* xs, c
 //     copies the 8-row block w of each limb, rows paired and 16-byte chunks swizzled), the packed
 //     weights by stage pairs (each thread copies the two words it decodes, one per stage), the
 //     tile's scales (all groups) once before the loop;
-//   - one stage ahead of its use each thread decodes its word through the byte table into the B
+//   - one stage ahead of its use each thread decodes its word (nibbles_bf16_16th) into the B
 //     layout of pipe_b_slot, conflict-free for the writes and the MFMA reads;
 //   - iteration t copies stage t + 4 into slot t % 4 and on even t the stage pair t + 4, t + 5,
 //     then runs stage t's chain with, between its MFMAs, stage t - 1's fold, the operand reads of
@@ -708,9 +708,6 @@ constexpr int kMidWaves = 8;
 constexpr int kMidGroupsMax = 128;  // scale groups per column held in LDS (K <= 4096)
 
 struct MidLds {
-    // byte b of packed weights -> the bf16 values v / 16 of its low and high nibbles (low and high
-    // half); first, so that ds_read's 16-bit offset field reaches it from a byte-scaled address
-    uint32_t lut[256];
     u32x4 a[kMidStages][kLimbs][8][64];      // stage, limb, 8-row block, 16-byte chunk (row pairs)
     uint32_t braw[2][kMidWaves][2][64];      // stage-pair slot, wavefront, stage of the pair, thread
     u32x4 b[2][2][2][2][64];                 // stage parity, group of the stage, 32-column tile, half, slot
@@ -808,12 +805,10 @@ __global__ __launch_bounds__(64 * kMidWaves) void q4_gemm_mid_kernel(const uint1
                                              0, 0);
     };
     auto decode_word = [&](int t) { return lds.braw[(t >> 1) & 1][wid][t & 1][lane]; };
-    auto decode_lookup = [&](uint32_t wd, u32x4& v) {  // one table entry per byte (two values)
-        typedef __attribute__((address_space(3))) const volatile uint32_t lds_word;
-        lds_word* lut = (lds_word*)(&lds.lut[0]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = lut[(wd >> (8 * j)) & 0xFFu];
-    };
+    // VALU decode (13 instructions per word): in this kernel, which waits on LDS more than it issues,
+    // it measured faster than the wide kernel's byte table, whose reads land on random banks
+    // (24.2 against 26.0-26.6 us per call at 1024^3).
+    auto decode_lookup = [&](uint32_t wd, u32x4& v) { v = nibbles_bf16_16th(wd); };
     auto decode_write = [&](int t, const u32x4& v) { lds.b[t & 1][bu][bc >> 5][bw >> 1][bdst] = v; };
     auto barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
@@ -835,13 +830,8 @@ __global__ __launch_bounds__(64 * kMidWaves) void q4_gemm_mid_kernel(const uint1
     issue(min(2, T - 1), 2);
     issue_b(min(1, jmax), 1);
     issue(min(3, T - 1), 3);
-    if (tid < 256) {  // the byte table, the same conversions as nibbles_bf16_16th
-        const uint32_t lo = __float_as_uint(__builtin_amdgcn_cvt_off_f32_i4(tid));
-        const uint32_t hi = __float_as_uint(__builtin_amdgcn_cvt_off_f32_i4(tid >> 4));
-        lds.lut[tid] = (lo >> 16) | (hi & 0xFFFF0000u);
-    }
     asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    barrier();  // scales and table visible, every wavefront's stages 0 and 1 and pair 0 copied
+    barrier();  // scales visible, every wavefront's stages 0 and 1 and pair 0 copied
     {
         u32x4 v0, v1;
         const uint32_t w0 = decode_word(0), w1 = decode_word(1);
