@@ -711,7 +711,9 @@ struct MidLds {
     u32x4 a[kMidStages][kLimbs][8][64];      // stage, limb, 8-row block, 16-byte chunk (row pairs)
     uint32_t braw[2][kMidWaves][2][64];      // stage-pair slot, wavefront, stage of the pair, thread
     u32x4 b[2][2][2][2][64];                 // stage parity, group of the stage, 32-column tile, half, slot
-    float s[kMidTile * kMidGroupsMax + 64];  // tile column, group (as in the array); copy slack
+    // the tile's scales as they lie in the array (column, group), one padding word after every 64:
+    // value i at i + i / 64, so the 32 columns one read touches fall in distinct banks
+    float s[kMidTile * kMidGroupsMax + kMidGroupsMax + 64];
 };
 static_assert(sizeof(MidLds) <= 160 * 1024, "LDS budget");
 
@@ -821,7 +823,7 @@ __global__ __launch_bounds__(64 * kMidWaves) void q4_gemm_mid_kernel(const uint1
         const size_t last = static_cast<size_t>(N - nt0) * G * 4 - 4;
         for (int b = wid; 64 * b < units; b += kMidWaves)  // uniform
             __builtin_amdgcn_global_load_lds(ssrc + min(static_cast<size_t>(4 * (64 * b + lane)), last),
-                                             reinterpret_cast<char*>(lds.s) + 256 * b, 4, 0, 0);
+                                             reinterpret_cast<char*>(lds.s) + 260 * b, 4, 0, 0);
     }
     const int jmax = (T - 1) / 2;  // the last stage pair
     issue(0, 0);
@@ -891,7 +893,7 @@ __global__ __launch_bounds__(64 * kMidWaves) void q4_gemm_mid_kernel(const uint1
             acc[o] = fma(r.s, pd[o & 1], acc[o]);
         }
     };
-    const float* srow = lds.s + (32 * wn + col32) * G + ku;  // this lane's column, group ku of stage 0
+    const int sbase = (32 * wn + col32) * G + ku;  // this lane's column, group ku of stage 0 (unpadded index)
 
     for (int t0 = 0; t0 < T; t0 += 2) {
         static_for<2>([&](auto uc) {
@@ -921,7 +923,8 @@ __global__ __launch_bounds__(64 * kMidWaves) void q4_gemm_mid_kernel(const uint1
                         // t + 3, t + 4 and one pair (3 + 3 + 2 copies)
                         asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
                         wd = decode_word(t + 2);
-                        sraw = srow[2 * t];
+                        const int si = sbase + 2 * t;
+                        sraw = lds.s[si + (si >> 6)];
                     }
                     if constexpr (i == 1) decode_lookup(wd, dec);
                     if constexpr (i == 5) decode_write(t + 2, dec);  // past the last stage: an unread buffer
