@@ -15,6 +15,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <atomic>
 #include <exception>
 #include <mutex>
 #include <new>
@@ -87,16 +88,22 @@ constexpr int kMaxDevices = 64;
 std::mutex g_device_mutex;
 DeviceState g_devices[kMaxDevices];
 
-// Number of visible devices, queried once (the set of devices is fixed for the process).
+// Number of visible devices, queried once (the set of devices is fixed for the process). The
+// cache is written under g_device_mutex, so threads that race on the first call all see one
+// value; a failed query is not cached and is retried by the next call.
 int device_count() {
-    static int cached = -1;
-    if (cached < 0) {
-        int count = 0;
-        hipError_t e = hipGetDeviceCount(&count);
-        if (e != hipSuccess || count <= 0) throw HipError{e == hipSuccess ? hipErrorNoDevice : e, "no HIP device"};
-        cached = count < kMaxDevices ? count : kMaxDevices;
-    }
-    return cached;
+    static std::atomic<int> cached{-1};
+    int c = cached.load(std::memory_order_acquire);
+    if (c > 0) return c;
+    std::lock_guard<std::mutex> lock(g_device_mutex);
+    c = cached.load(std::memory_order_relaxed);
+    if (c > 0) return c;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count <= 0) throw HipError{e == hipSuccess ? hipErrorNoDevice : e, "no HIP device"};
+    c = count < kMaxDevices ? count : kMaxDevices;
+    cached.store(c, std::memory_order_release);
+    return c;
 }
 
 DeviceState& current_device() {
@@ -239,8 +246,6 @@ int run_host(const float* x, const uint8_t* w, const float* s, const uint8_t* d_
     return ok();
 }
 
-// Returns SPACESLUG_ERR_UNSUPPORTED (with a message) when `st` is being captured into a graph,
-// else 0. For the calls that use the shared, grow-only workspace.
 // The event that orders workspace users across streams of one device. It only orders GPU work on
 // that device (hipStreamWaitEvent), so it is recorded without the system-scope memory fence a
 // default event performs on completion, which cost several microseconds of stream time per call.
@@ -249,6 +254,8 @@ void create_ws_event(DeviceState& dev) {
           "hipEventCreateWithFlags");
 }
 
+// Returns SPACESLUG_ERR_UNSUPPORTED (with a message) when `st` is being captured into a graph,
+// else 0. For the calls that use the shared, grow-only workspace.
 int refuse_capture(hipStream_t st, const char* what) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     check(hipStreamIsCapturing(st, &cs), "hipStreamIsCapturing");
