@@ -25,7 +25,7 @@ PROBES_SOURCE = "bench_probes.hip"
 PROBES_LIB_NAME = "libspaceslug_probes.so"
 ARCH = "gfx950"
 
-SOURCES = ["q4_gemv.hip", "q4_gemm.hip", "q4_quantize.hip", "cq4.hip", "sgemm.hip", "runtime_abi.cpp"]
+SOURCES = ["q4_gemv.hip", "q4_gemm.hip", "q4_small.hip", "q4_quantize.hip", "cq4.hip", "sgemm.hip", "runtime_abi.cpp"]
 
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}",

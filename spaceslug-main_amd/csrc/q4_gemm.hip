@@ -1,21 +1,17 @@
-// MFMA int4 GEMM for 5+ rows (prefill, small-batch decode, LoRA projections).
-// Four kernels: q4_gemm_wide_kernel for M > 32, q4_gemm_mid_kernel for M > 32
-// shapes whose wide grid would need a K-split, q4_gemm_skinny_kernel for
-// M <= 32 with K % 128 == 0 and q4_gemm_mfma_kernel (K-split) for the other
-// M <= 32 shapes, each described at its definition.
+// MFMA int4 GEMM for more than 32 rows (prefill, LoRA projections, the reference's
+// 1024^3 bench shape). Two kernels: q4_gemm_wide_kernel, and q4_gemm_mid_kernel for
+// the shapes whose wide grid would need a K-split, each described at its definition.
+// (Up to 32 rows the exact small-batch GEMM of q4_small.hip runs instead.)
 //
 // Replaces q4gemm.comp:61-175 (64x64 tile, LDS-staged dequantised B, 4x4 FMA
-// micro-tile per thread) with a CDNA4 design on the matrix cores: the two
-// small-M kernels on v_mfma_f32_16x16x4_f32, the wide and mid-size kernels on
-// v_mfma_f32_32x32x16_bf16 with x split exactly into three bf16 limbs.
-// Common to all of them:
+// micro-tile per thread) with a CDNA4 design on the matrix cores:
+// v_mfma_f32_32x32x16_bf16 with x split exactly into three bf16 limbs. Common to both:
 //   - per 32-value scale group, each lane feeds the MFMA K slots with 8
 //     consecutive K values, so its B operands for one column are the 8 nibbles
 //     of ONE 32-bit word of the packed column and its A operands are 8
-//     consecutive values of one row. Weights are decoded to v / 16
-//     (v_cvt_off_f32_i4, exact; the factor 16 joins the scale or multiplies the
-//     float64 sums at the store);
-//   - every product x * v / 16 is exact in fp32; the MFMA accumulates
+//     consecutive values of one row. Weights are decoded to v / 16 (exact in
+//     bf16; the factor 16 multiplies the float64 sums at the store);
+//   - every product limb * v / 16 is exact in fp32; the MFMA accumulates
 //     P = sum x * v / 16 over one group in fp32 from zero, and the group is
 //     folded straight into a float64 accumulator as s * P. Scale application
 //     moves out of the inner loop, the long K sum is carried in double, and the
@@ -35,205 +31,10 @@
 
 #include "q4_device.hpp"
 #include "q4_kernels.hpp"
+#include "q4_lora.hpp"
 
 namespace spaceslug {
 namespace {
-
-template <int WM, int WN, int WAVES_M, int WAVES_N>
-struct TileShape {
-    static constexpr int kWaves = WAVES_M * WAVES_N;
-    static constexpr int kThreads = 64 * kWaves;
-    static constexpr int kBM = 16 * WM * WAVES_M;
-    static constexpr int kBN = 16 * WN * WAVES_N;
-};
-
-// Maps the linear workgroup id to (tile_n, tile_m) so that consecutive ids on
-// one XCD (hardware dispatches workgroup i to XCD i % 8) cover a contiguous
-// run of tiles, walked M-fastest inside column bands.
-__device__ __forceinline__ void xcd_tile(int tiles_m, int tiles_n, int& tm, int& tn) {
-    const int total = tiles_m * tiles_n;
-    const int id = blockIdx.x;
-    int lin = id;
-    if (total >= 64 && (total & 7) == 0) {
-        const int per_xcd = total >> 3;
-        lin = (id & 7) * per_xcd + (id >> 3);
-    }
-    tm = lin % tiles_m;
-    tn = lin / tiles_m;
-}
-
-// T[row][r] = the sum of its t_splits partials, in double and in split order, rounded once.
-__device__ __forceinline__ float lora_t_value(const float* __restrict__ tpart, int t_splits, int M, int R, int row,
-                                              int r) {
-    double t = 0.0;
-    for (int z = 0; z < t_splits; ++z) t += static_cast<double>(tpart[(static_cast<size_t>(z) * M + row) * R + r]);
-    return static_cast<float>(t);
-}
-
-// Operands of one 32-value group for a wavefront's WM x WN tiles.
-template <int WM, int WN>
-struct GroupOps {
-    f32x4 alo[WM], ahi[WM];  // x[row j][8q .. 8q+7] of each M tile
-    uint32_t bw[WN];         // packed word q of column j's group, each N tile
-    float bs[WN];            // scale of column j's group, each N tile
-};
-
-template <int WM, int WN>
-__device__ __forceinline__ void load_group(GroupOps<WM, WN>& o, const float* const (&arow)[WM],
-                                           const uint32_t* const (&bcol)[WN], const float* const (&scol)[WN], int g) {
-#pragma unroll
-    for (int tm = 0; tm < WM; ++tm) {
-        o.alo[tm] = *reinterpret_cast<const f32x4*>(arow[tm] + g * 32);
-        o.ahi[tm] = *reinterpret_cast<const f32x4*>(arow[tm] + g * 32 + 4);
-    }
-#pragma unroll
-    for (int tn = 0; tn < WN; ++tn) {
-        o.bw[tn] = bcol[tn][g * 4];
-        o.bs[tn] = scol[tn][g];
-    }
-}
-
-// K-split kernel for the small-M shapes the skinny kernel does not take
-// (M <= 32, K % 128 != 0): a wavefront owns a (16*WM) x (16*WN) output block,
-// its A operands (two 128-bit loads of row j per group) and weight words go
-// global -> VGPR, and PD groups are in flight behind the one being computed.
-template <int WM, int WN, int WAVES_M, int WAVES_N, int PD>
-// x, wq and ws are deliberately not __restrict__: as provably invariant loads
-// the compiler would be free to re-issue the prefetched group's loads at their
-// use (to save registers), which serialises them behind the compute.
-__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void q4_gemm_mfma_kernel(
-    const float* x, const uint32_t* wq, const float* ws, float* __restrict__ out, int M, int N, int K, int tiles_m,
-    int tiles_n, int groups_per_split, const float* __restrict__ tpart, int t_splits, const float* __restrict__ lb,
-    int R,
-    float lscale) {
-    using Shape = TileShape<WM, WN, WAVES_M, WAVES_N>;
-    const int lane = threadIdx.x & 63;
-    const int wid = threadIdx.x >> 6;
-    const int wm = wid % WAVES_M;
-    const int wn = wid / WAVES_M;
-    const int j = lane & 15;
-    const int q = lane >> 4;
-    const int G = K >> 5;
-
-    int tile_m, tile_n;
-    xcd_tile(tiles_m, tiles_n, tile_m, tile_n);
-    const int m0 = tile_m * Shape::kBM + wm * 16 * WM;
-    const int n0 = tile_n * Shape::kBN + wn * 16 * WN;
-    const int g_begin = blockIdx.y * groups_per_split;
-    const int g_end = min(G, g_begin + groups_per_split);
-
-    const float* arow[WM];
-#pragma unroll
-    for (int tm = 0; tm < WM; ++tm) {
-        const int row = min(m0 + 16 * tm + j, M - 1);
-        arow[tm] = x + static_cast<size_t>(row) * K + 8 * q;
-    }
-    const uint32_t* bcol[WN];
-    const float* scol[WN];
-#pragma unroll
-    for (int tn = 0; tn < WN; ++tn) {
-        const int col = min(n0 + 16 * tn + j, N - 1);
-        bcol[tn] = wq + static_cast<size_t>(col) * (K >> 3) + q;
-        scol[tn] = ws + static_cast<size_t>(col) * G;
-    }
-
-    double acc[WM][WN][4];
-#pragma unroll
-    for (int tm = 0; tm < WM; ++tm)
-#pragma unroll
-        for (int tn = 0; tn < WN; ++tn)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[tm][tn][i] = 0.0;
-
-    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-    // One group: P = x * v over 32 K values on the MFMA from zero, then acc += s * P.
-    auto do_group = [&](const GroupOps<WM, WN>& o) {
-        f32x4 P[WM][WN];
-        float bv[WN][8];
-#pragma unroll
-        for (int tn = 0; tn < WN; ++tn) nibbles_signed_16th_mfma(o.bw[tn], bv[tn]);
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-#pragma unroll
-            for (int tm = 0; tm < WM; ++tm) {
-                const float av = t < 4 ? o.alo[tm][t & 3] : o.ahi[tm][t & 3];
-#pragma unroll
-                for (int tn = 0; tn < WN; ++tn)
-                    P[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[tn][t], t == 0 ? zero : P[tm][tn], 0, 0, 0);
-            }
-        }
-#pragma unroll
-        for (int tn = 0; tn < WN; ++tn) {
-            const double sc = static_cast<double>(o.bs[tn]) * kSixteenthsUnit;
-#pragma unroll
-            for (int tm = 0; tm < WM; ++tm)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[tm][tn][i] = fma(sc, static_cast<double>(P[tm][tn][i]), acc[tm][tn][i]);
-        }
-    };
-    if (g_begin < g_end) {
-        // PD + 1 buffers used in rotation: while buffer s computes group g+s,
-        // buffer (s+PD) % (PD+1) receives group g+s+PD, so PD groups are in flight
-        // behind the one being computed. The rotation is unrolled, so no buffer
-        // is copied (a register copy would wait for its loads). Loads past the
-        // split are clamped to its last group and never accumulated.
-        constexpr int NB = PD + 1;
-        GroupOps<WM, WN> buf[NB];
-#pragma unroll
-        for (int p = 0; p < PD; ++p) {
-            load_group<WM, WN>(buf[p], arow, bcol, scol, min(g_begin + p, g_end - 1));
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        for (int g = g_begin; g < g_end; g += NB) {
-#pragma unroll
-            for (int sl = 0; sl < NB; ++sl) {
-                load_group<WM, WN>(buf[(sl + PD) % NB], arow, bcol, scol, min(g + sl + PD, g_end - 1));
-                __builtin_amdgcn_sched_barrier(0);
-                if (g + sl < g_end) do_group(buf[sl]);  // uniform across the workgroup
-                // keep the next slot's loads and work below this point so each slot
-                // waits only for its own loads
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-    }
-
-    if (lb != nullptr && blockIdx.y == 0) {
-        // LoRA epilogue: + lscale * T[m0.., :R] * lb[:R, n0..] on the MFMA, r in the K slot
-        // (T = x * la, M x R, summed by lora_t_reduce_kernel).
-#pragma unroll
-        for (int tm = 0; tm < WM; ++tm) {
-            const int row = min(m0 + 16 * tm + j, M - 1);
-#pragma unroll
-            for (int tn = 0; tn < WN; ++tn) {
-                const int col = min(n0 + 16 * tn + j, N - 1);
-                f32x4 P = zero;
-                for (int r0 = 0; r0 < R; r0 += 4) {
-                    const int r = r0 + q;
-                    const float av = r < R ? lora_t_value(tpart, t_splits, M, R, row, r) : 0.0f;
-                    const float bv = r < R ? lb[static_cast<size_t>(r) * N + col] : 0.0f;
-                    P = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, P, 0, 0, 0);
-                }
-                const double s = static_cast<double>(lscale);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[tm][tn][i] = fma(s, static_cast<double>(P[i]), acc[tm][tn][i]);
-            }
-        }
-    }
-
-    float* dst = out + static_cast<size_t>(blockIdx.y) * M * N;
-#pragma unroll
-    for (int tm = 0; tm < WM; ++tm) {
-#pragma unroll
-        for (int tn = 0; tn < WN; ++tn) {
-            const int col = n0 + 16 * tn + j;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int row = m0 + 16 * tm + 4 * q + i;
-                if (row < M && col < N) dst[static_cast<size_t>(row) * N + col] = static_cast<float>(acc[tm][tn][i]);
-            }
-        }
-    }
-}
 
 // Calls f(std::integral_constant<int, I>{}) for I = 0 .. N-1 in order (compile-time indices, so
 // register arrays indexed by I stay in registers).
@@ -756,7 +557,8 @@ __global__ __launch_bounds__(256) void x_limb_rows_kernel(const float* __restric
     for (int li = 0; li < kLimbs; ++li) *reinterpret_cast<u32x4*>(dst + li * 64) = limb[li];
 }
 
-// x, wq and ws are not __restrict__ for the reason given at q4_gemm_mfma_kernel.
+// x limbs, wq and ws are deliberately not __restrict__: as provably invariant loads the compiler
+// would be free to re-issue loads at their use (to save registers), serialising them behind compute.
 __global__ __launch_bounds__(64 * kMidWaves) void q4_gemm_mid_kernel(const uint16_t* xs, const uint32_t* wq,
                                                                     const float* ws, float* __restrict__ y, int M,
                                                                     int N, int K, int tiles_m) {
@@ -995,70 +797,6 @@ __global__ __launch_bounds__(64 * kMidWaves) void q4_gemm_mid_kernel(const uint1
     }
 }
 
-// LoRA pre-pass on the MFMA: tpart[z][m][r] = sum over the kLoraGroupsPerBlock groups
-// of split z of x[m][k] * la[k][r] (la is K x R row-major). One workgroup of 4
-// wavefronts per 16 x 16 tile of (rows, ranks) and split; each wavefront takes
-// kLoraGroupsPerWave groups with all of its operands loaded before its first MFMA,
-// and the four sums are added through LDS in wavefront order. The GEMM epilogues
-// add the t_splits partials of T (lora_t_value), so T needs no reduction launch.
-constexpr int kLoraGroupsPerWave = 8;
-constexpr int kLoraGroupsPerBlock = 4 * kLoraGroupsPerWave;
-
-__device__ __forceinline__ void lora_t_block(const float* __restrict__ x, const float* __restrict__ la,
-                                             float* __restrict__ tpart, int M, int K, int R, int bx, int by,
-                                             int bz) {
-    __shared__ f32x4 red[4][64];
-    const int lane = threadIdx.x & 63;
-    const int w = threadIdx.x >> 6;
-    const int j = lane & 15;
-    const int q = lane >> 4;
-    const int G = K >> 5;
-    const int m0 = bx * 16;
-    const int r0 = by * 16;
-    const int g_begin = bz * kLoraGroupsPerBlock + w * kLoraGroupsPerWave;
-    const int row = min(m0 + j, M - 1);
-    const int r = r0 + j;
-    const int rc = min(r, R - 1);
-    const float* xr = x + static_cast<size_t>(row) * K + 8 * q;
-
-    f32x4 a_lo[kLoraGroupsPerWave], a_hi[kLoraGroupsPerWave];
-    float b[kLoraGroupsPerWave][8];
-#pragma unroll
-    for (int i = 0; i < kLoraGroupsPerWave; ++i) {
-        const int g = min(g_begin + i, G - 1);
-        a_lo[i] = *reinterpret_cast<const f32x4*>(xr + g * 32);
-        a_hi[i] = *reinterpret_cast<const f32x4*>(xr + g * 32 + 4);
-        const float* lr = la + static_cast<size_t>(g * 32 + 8 * q) * R + rc;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) b[i][t] = lr[static_cast<size_t>(t) * R];
-    }
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int i = 0; i < kLoraGroupsPerWave; ++i) {
-        if (g_begin + i < G) {  // uniform per wavefront
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                const float av = t < 4 ? a_lo[i][t & 3] : a_hi[i][t & 3];
-                const float bv = r < R ? b[i][t] : 0.0f;
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
-            }
-        }
-    }
-    red[w][lane] = acc;
-    __syncthreads();
-    if (w == 0) {
-        f32x4 sum = red[0][lane];
-#pragma unroll
-        for (int v = 1; v < 4; ++v) sum += red[v][lane];
-        float* dst = tpart + static_cast<size_t>(bz) * M * R;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int rr = m0 + 4 * q + i;
-            if (rr < M && r < R) dst[static_cast<size_t>(rr) * R + r] = sum[i];
-        }
-    }
-}
-
 // One launch that prepares a call's GEMM: the first lora_blocks workgroups compute the LoRA T
 // partials (lora_t_block, grid tiles_m_t x tiles_r x t_splits), the rest split x into bf16
 // limbs (split_x_block; none when the GEMM reads fp32 x). Both only read x. The T workgroups
@@ -1073,195 +811,6 @@ __global__ __launch_bounds__(256) void prep_kernel(const float* __restrict__ x, 
         return;
     }
     lora_t_block(x, la, tpart, M, K, R, b % tiles_m_t, (b / tiles_m_t) % tiles_r, b / (tiles_m_t * tiles_r));
-}
-
-// Small-M GEMM (M <= 32, K % 128 == 0) with no K-split partials in memory: a
-// workgroup owns one 16 x 16 output tile and its KW wavefronts split K between
-// them; their float64 accumulators are summed through LDS in wavefront order
-// (deterministic), and the LoRA term, if any, is added in double before the
-// single store. Per wavefront, weights and scales move in units of 4 groups (a
-// "quad"): lane (j, q) loads column j's 16 bytes of group 4*quad + q (one
-// 128-bit load; the 4 lanes of a column read 64 contiguous bytes) and its
-// scale, then a 4 x 4 transpose across the 16-lane rows (v_permlane*_swap)
-// gives every lane word q of each of the 4 groups, the MFMA B layout. Two quads
-// are in flight while one computes (statically named buffers E and O); the
-// pipeline issues no load past the wavefront's last quad. KW is 16 when the
-// tile grid has no more workgroups than the chip has CUs (16 wavefronts per CU
-// from one tile), else 8. Above 8 rows x reaches the MFMA through LDS (below).
-// Measured at M=16, K=N=4096: 10.9 us per call with x staged (12.5 us with x
-// loaded directly, 14.2 us with 8 wavefronts), against 20.5 us for the split-K
-// kernel plus its reduction.
-constexpr int kSkinnyWavesFew = 16;
-constexpr int kSkinnyWavesMany = 8;
-// Rows up to which x goes global -> VGPR directly; taller tiles copy it through LDS.
-constexpr int kSkinnyDirectMaxRows = 8;
-
-// Per-quad operands of one wavefront: x for the quad's 4 groups (in registers
-// straight from global memory, or copied through LDS first, below) and the
-// weights and scales of its column.
-struct QuadW {
-    u32x4 bw;  // column j, group 4 * quad + q: its 16 packed bytes
-    float bs;  // scale of column j, group 4 * quad + q
-};
-
-__device__ __forceinline__ void load_quad_w(QuadW& o, const u32x4* bq, const float* sq, int qi) {
-    o.bw = __builtin_nontemporal_load(bq + 4 * qi);
-    o.bs = __builtin_nontemporal_load(sq + 4 * qi);
-}
-
-// x[row j][32 g + 8 q .. +7] for the quad's 4 groups: two 128-bit loads per group, each
-// instruction touching half of 16 rows' 128-byte lines.
-__device__ __forceinline__ void load_quad_x(f32x4 (&alo)[4], f32x4 (&ahi)[4], const float* arow, int qi) {
-#pragma unroll
-    for (int gi = 0; gi < 4; ++gi) {
-        alo[gi] = *reinterpret_cast<const f32x4*>(arow + (4 * qi + gi) * 32);
-        ahi[gi] = *reinterpret_cast<const f32x4*>(arow + (4 * qi + gi) * 32 + 4);
-    }
-}
-
-__device__ __forceinline__ void mma_quad(const QuadW& o, const f32x4 (&alo)[4], const f32x4 (&ahi)[4],
-                                         double (&acc)[4]) {
-    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-    const u32x4 bw = transpose_rows(o.bw);  // word q of each of the quad's groups
-    const f32x4 bs = gather_rows(o.bs);     // the quad's 4 scales of column j
-#pragma unroll
-    for (int gi = 0; gi < 4; ++gi) {
-        float bv[8];
-        nibbles_signed_16th_mfma(bw[gi], bv);
-        f32x4 P;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const float av = t < 4 ? alo[gi][t & 3] : ahi[gi][t & 3];
-            P = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[t], t == 0 ? zero : P, 0, 0, 0);
-        }
-        const double sc = static_cast<double>(bs[gi]) * kSixteenthsUnit;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[r] = fma(sc, static_cast<double>(P[r]), acc[r]);
-    }
-}
-
-// With kStageX, each wavefront copies its quad of x (16 rows x 128 floats, 8 KiB)
-// global -> LDS by global_load_lds_dwordx4, two full 512-byte row runs per
-// instruction, and reads its MFMA operands from there: the register-direct loads
-// above touch twice the cache lines for the same bytes, which at 16 rows (x read
-// whole by every CU) cost 13% of the kernel (M=16, K=N=4096: 12.5 -> 10.9 us).
-// Row j's 16-byte chunk c (k = 4 c .. 4 c + 3 of the quad) sits at chunk c ^ j of
-// the row, so a pass of 16 lanes reading one chunk of each row hits 16 distinct
-// bank groups. The next quad's copy starts once this quad's operands are in
-// registers. At M <= 8 the copy moves rows the tile does not use and the direct
-// loads are faster (M=5: 9.9 against 10.7 us).
-constexpr int kQuadXFloats = 16 * 128;
-
-template <int KW, bool kStageX>
-// x, wq and ws are not __restrict__ for the reason given at q4_gemm_mfma_kernel.
-__global__ __launch_bounds__(64 * KW) void q4_gemm_skinny_kernel(const float* x, const uint32_t* wq, const float* ws,
-                                                                float* __restrict__ y, int M, int N, int K,
-                                                                int tiles_m, const float* __restrict__ tpart,
-                                                                int t_splits,
-                                                                const float* __restrict__ lb, int R, float lscale) {
-    // Per wavefront: its x unit (staged form), then 256 partial sums in double.
-    constexpr int kRegionFloats = kStageX ? kQuadXFloats : 512;
-    __shared__ f32x4 smem[KW * kRegionFloats / 4];
-    const int lane = threadIdx.x & 63;
-    const int wk = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-    const int j = lane & 15;
-    const int q = lane >> 4;
-    const int G = K >> 5;
-    const int Q = G >> 2;
-    const int m0 = (blockIdx.x % tiles_m) * 16;
-    const int n0 = (blockIdx.x / tiles_m) * 16;
-    const int qpw = (Q + KW - 1) / KW;
-    const int qb = wk * qpw;
-    const int qe = min(Q, qb + qpw);
-    const int col = min(n0 + j, N - 1);
-    const u32x4* bq = reinterpret_cast<const u32x4*>(wq + static_cast<size_t>(col) * (K >> 3)) + q;
-    const float* sq = ws + static_cast<size_t>(col) * G + q;
-    const float* arow = x + static_cast<size_t>(min(m0 + j, M - 1)) * K + 8 * q;
-    float* xs = reinterpret_cast<float*>(smem) + wk * kRegionFloats;
-
-    // Staged copy: instruction i moves rows 2i and 2i+1; lane l fetches the chunk that
-    // lands at position l & 31 of row 2i + (l >> 5).
-    const float* xsrc[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int r = 2 * i + (lane >> 5);
-        xsrc[i] = x + static_cast<size_t>(min(m0 + r, M - 1)) * K + 4 * ((lane & 31) ^ r);
-    }
-    auto issue_x = [&](int qi) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) __builtin_amdgcn_global_load_lds(xsrc[i] + qi * 128, xs + i * 256, 16, 0, 0);
-    };
-    auto stage_start = [&](int qi) {
-        if constexpr (kStageX) issue_x(qi);
-    };
-    // One quad: its x operands (staged: wait for the copy, read LDS, start the next copy
-    // into the same bytes), then the MFMAs.
-    auto step = [&](const QuadW& w, int qi, double (&acc)[4]) {
-        f32x4 alo[4], ahi[4];
-        if constexpr (kStageX) {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-#pragma unroll
-            for (int gi = 0; gi < 4; ++gi) {
-                alo[gi] = *reinterpret_cast<const f32x4*>(xs + j * 128 + (((8 * gi + 2 * q) ^ j) << 2));
-                ahi[gi] = *reinterpret_cast<const f32x4*>(xs + j * 128 + (((8 * gi + 2 * q + 1) ^ j) << 2));
-            }
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            if (qi + 1 < qe) issue_x(qi + 1);  // uniform
-        } else {
-            load_quad_x(alo, ahi, arow, qi);
-        }
-        mma_quad(w, alo, ahi, acc);
-    };
-
-    double acc[4] = {0.0, 0.0, 0.0, 0.0};
-    if (qb < qe) {  // every condition below is uniform per wavefront
-        QuadW E, O;
-        stage_start(qb);
-        load_quad_w(E, bq, sq, qb);
-        if (qb + 1 < qe) load_quad_w(O, bq, sq, qb + 1);
-        for (int qi = qb; qi < qe; qi += 2) {
-            step(E, qi, acc);
-            if (qi + 2 < qe) load_quad_w(E, bq, sq, qi + 2);
-            if (qi + 1 < qe) {
-                step(O, qi + 1, acc);
-                if (qi + 3 < qe) load_quad_w(O, bq, sq, qi + 3);
-            }
-        }
-    }
-
-    // Partial sums through the wavefront's own LDS region (no copy is in flight any
-    // more), summed in wavefront order.
-    double* red = reinterpret_cast<double*>(smem);
-    constexpr int kRedStride = kRegionFloats / 2;  // doubles per wavefront region
-#pragma unroll
-    for (int r = 0; r < 4; ++r) red[wk * kRedStride + (4 * q + r) * 16 + j] = acc[r];
-    // LoRA: the tile's 16 rows of T (R values each, their partials summed) and 16 columns of lb,
-    // loaded by the whole workgroup at once rather than one dependent pair per rank per output.
-    __shared__ float lora_t_s[16 * kMaxLoraRank];
-    __shared__ float lora_b_s[kMaxLoraRank * 16];
-    if (lb != nullptr) {
-        for (int e = threadIdx.x; e < 16 * R; e += 64 * KW) {
-            lora_t_s[e] = lora_t_value(tpart, t_splits, M, R, min(m0 + e / R, M - 1), e % R);
-            lora_b_s[e] = lb[static_cast<size_t>(e >> 4) * N + min(n0 + (e & 15), N - 1)];
-        }
-    }
-    __syncthreads();
-    for (int e = threadIdx.x; e < 256; e += 64 * KW) {
-        const int rr = m0 + (e >> 4);
-        const int cc = n0 + (e & 15);
-        if (rr >= M || cc >= N) continue;
-        double s = 0.0;
-#pragma unroll
-        for (int w = 0; w < KW; ++w) s += red[w * kRedStride + e];
-        if (lb != nullptr) {
-            double t = 0.0;
-            for (int r = 0; r < R; ++r)
-                t = fma(static_cast<double>(lora_t_s[(e >> 4) * R + r]), static_cast<double>(lora_b_s[r * 16 + (e & 15)]),
-                        t);
-            s = fma(static_cast<double>(lscale), t, s);
-        }
-        y[static_cast<size_t>(rr) * N + cc] = static_cast<float>(s);
-    }
 }
 
 // y[i] = sum_s part[s][i], in ascending s, accumulated in double (K-split
@@ -1286,29 +835,6 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
     }
 }
 
-template <int WM, int WN, int WAVES_M, int WAVES_N, int PD>
-hipError_t launch_mfma(const float* x, const uint8_t* w_packed, const float* w_scales, float* out,
-                       uint32_t m, uint32_t n, uint32_t k, int splits, const float* tpart, int t_splits,
-                       const float* lb,
-                       uint32_t rank, float lscale, hipStream_t stream) {
-    using Shape = TileShape<WM, WN, WAVES_M, WAVES_N>;
-    const int tiles_m = static_cast<int>((m + Shape::kBM - 1) / Shape::kBM);
-    const int tiles_n = static_cast<int>((n + Shape::kBN - 1) / Shape::kBN);
-    const int G = static_cast<int>(k / kGroup);
-    const int gps = (G + splits - 1) / splits;
-    hipLaunchKernelGGL((q4_gemm_mfma_kernel<WM, WN, WAVES_M, WAVES_N, PD>),
-                       dim3(tiles_m * tiles_n, splits), dim3(Shape::kThreads), 0, stream, x,
-                       reinterpret_cast<const uint32_t*>(w_packed), w_scales, out,
-                       static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), tiles_m,
-                       tiles_n, gps, tpart, t_splits, lb, static_cast<int>(rank), lscale);
-    return hipGetLastError();
-}
-
-// Tile shape of q4_gemm_mfma_kernel (M <= 32 with K not a multiple of 128): one
-// 16-row MFMA tile x 256 columns per workgroup (4 waves of 16 x 64), 2 groups in
-// flight.
-using SkinnyShape = TileShape<1, 4, 1, 4>;
-constexpr int kSkinnyPD = 2;
 // Wide tile of q4_gemm_wide_kernel: 128 x 128 outputs, 8 wavefronts.
 constexpr int kWideTile = 128;
 
@@ -1323,7 +849,7 @@ size_t split_x_bf16_bytes(uint32_t m, uint32_t k) {
 
 Q4Plan plan_q4gemm(const DeviceInfo& dev, uint32_t m, uint32_t n, uint32_t k, uint32_t rank) {
     Q4Plan plan{Q4Plan::kGemv, 1, 0, 0};
-    if (rank == 0 && m <= static_cast<uint32_t>(kGemvMaxRows)) {
+    if (rank == 0 && m == 1 && k / kGroup <= static_cast<uint32_t>(kGemvPipeMaxGroups)) {
         return plan;
     }
     const int groups = static_cast<int>(k / kGroup);
@@ -1332,30 +858,18 @@ Q4Plan plan_q4gemm(const DeviceInfo& dev, uint32_t m, uint32_t n, uint32_t k, ui
         plan.t_splits = (groups + kLoraGroupsPerBlock - 1) / kLoraGroupsPerBlock;
         lora_bytes += align_up(static_cast<size_t>(plan.t_splits) * m * rank * sizeof(float));  // T partials
     }
-    if (m <= 32 && k % (4 * kGroup) == 0) {
-        plan.kind = Q4Plan::kSkinny;  // K split inside the workgroup: no partials in memory
-        plan.workspace_bytes = lora_bytes;
+    if (m <= 32) {
+        plan.kind = Q4Plan::kDigits;
+        plan.workspace_bytes = align_up(digits_workspace_bytes(m, k)) + lora_bytes;
         return plan;
     }
-    int bm, bn, waves_per_tile;
-    if (m <= 32) {
-        plan.kind = Q4Plan::kSkinnySplitK;
-        bm = SkinnyShape::kBM;
-        bn = SkinnyShape::kBN;
-        waves_per_tile = SkinnyShape::kWaves;
-    } else {
-        plan.kind = Q4Plan::kWide;
-        bm = kWideTile;
-        bn = kWideTile;
-        waves_per_tile = kWideWavesPerTile;
-    }
-    const size_t tiles = static_cast<size_t>((m + bm - 1) / bm) * ((n + bn - 1) / bn);
-    const size_t waves = tiles * waves_per_tile;
-    // Resident wavefronts per SIMD: skinny 3 at its register count (2 targeted); wide 2 (one
-    // workgroup of 8 per CU, bound by LDS).
+    plan.kind = Q4Plan::kWide;
+    const size_t tiles = static_cast<size_t>((m + kWideTile - 1) / kWideTile) * ((n + kWideTile - 1) / kWideTile);
+    const size_t waves = tiles * kWideWavesPerTile;
+    // Resident wavefronts per SIMD: 2 (one workgroup of 8 per CU, bound by LDS).
     const size_t waves_per_simd = 2;
     const size_t target = 4 * waves_per_simd * static_cast<size_t>(dev.cu_count);
-    const int min_groups = plan.kind == Q4Plan::kSkinnySplitK ? 8 : 4;
+    const int min_groups = 4;
     int splits = 1;
     while (waves * splits * 2 <= target && groups / (splits * 2) >= min_groups) splits *= 2;
     // Re-derive so that no split is empty.
@@ -1363,15 +877,14 @@ Q4Plan plan_q4gemm(const DeviceInfo& dev, uint32_t m, uint32_t n, uint32_t k, ui
     splits = (groups + per_split - 1) / per_split;
     plan.splits = splits;
     const size_t mid_tiles = static_cast<size_t>((m + kMidTile - 1) / kMidTile) * ((n + kMidTile - 1) / kMidTile);
-    if (plan.kind == Q4Plan::kWide && splits > 1 && rank == 0 && k % 64 == 0 && groups <= kMidGroupsMax &&
+    if (splits > 1 && rank == 0 && k % 64 == 0 && groups <= kMidGroupsMax &&
         mid_tiles <= static_cast<size_t>(dev.cu_count)) {
         plan.kind = Q4Plan::kMid;  // whole K per 64 x 64 tile: no partials, no reduction launch
         plan.splits = 1;
         plan.workspace_bytes = align_up(static_cast<size_t>(m) * k * kLimbs * sizeof(uint16_t));  // x limbs
         return plan;
     }
-    size_t bytes = lora_bytes;
-    if (plan.kind == Q4Plan::kWide) bytes += align_up(split_x_bf16_bytes(m, k));  // x limbs
+    size_t bytes = lora_bytes + align_up(split_x_bf16_bytes(m, k));  // x limbs
     if (splits > 1) bytes += align_up(static_cast<size_t>(splits) * m * n * sizeof(float));
     plan.workspace_bytes = bytes;
     return plan;
@@ -1382,6 +895,9 @@ hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float*
                          uint32_t n, uint32_t k, const float* la, const float* lb, uint32_t rank,
                          float lora_scale, void* workspace, hipStream_t stream) {
     if (plan.kind == Q4Plan::kGemv) return launch_gemv(dev, x, w_packed, w_scales, y, m, n, k, stream);
+    if (plan.kind == Q4Plan::kDigits)
+        return launch_q4gemm_digits(dev, x, w_packed, w_scales, y, m, n, k, la, lb, rank, lora_scale, plan.t_splits,
+                                    workspace, stream);
     if (plan.kind == Q4Plan::kMid) {
         uint16_t* xs = static_cast<uint16_t*>(workspace);
         const int tiles_m = static_cast<int>((m + kMidTile - 1) / kMidTile);
@@ -1413,51 +929,28 @@ hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float*
     }
     const int kk = static_cast<int>(k), mm = static_cast<int>(m), rr = static_cast<int>(rank);
     // One preparation launch: the bf16 limbs of x for the wide kernel and/or the LoRA T partials.
-    uint16_t* xs = plan.kind == Q4Plan::kWide ? reinterpret_cast<uint16_t*>(wsp) : nullptr;
+    uint16_t* xs = reinterpret_cast<uint16_t*>(wsp);
     {
         // split_x_block: 64 threads per (16-row block, group)
-        const int split_blocks = xs ? static_cast<int>(((m + 15) / 16 * static_cast<size_t>(k / kGroup) * 64 + 255) / 256) : 0;
+        const int split_blocks = static_cast<int>(((m + 15) / 16 * static_cast<size_t>(k / kGroup) * 64 + 255) / 256);
         const int tiles_m_t = static_cast<int>((m + 15) / 16), tiles_r = static_cast<int>((rank + 15) / 16);
         const int lora_blocks = rank ? tiles_m_t * tiles_r * plan.t_splits : 0;
-        if (split_blocks + lora_blocks > 0) {
-            hipLaunchKernelGGL(prep_kernel, dim3(static_cast<unsigned>(split_blocks + lora_blocks)), dim3(256), 0,
-                               stream, x, xs, mm, kk, lora_blocks, la, tpart, rr, tiles_m_t, tiles_r);
-            const hipError_t pe = hipGetLastError();
-            if (pe != hipSuccess) return pe;
-        }
+        hipLaunchKernelGGL(prep_kernel, dim3(static_cast<unsigned>(split_blocks + lora_blocks)), dim3(256), 0, stream,
+                           x, xs, mm, kk, lora_blocks, la, tpart, rr, tiles_m_t, tiles_r);
+        const hipError_t pe = hipGetLastError();
+        if (pe != hipSuccess) return pe;
     }
     float* out = plan.splits > 1 ? partial : y;
     const float* lbp = rank ? lb : nullptr;
-    hipError_t e;
-    if (plan.kind == Q4Plan::kSkinny) {
-        const int tiles_m = static_cast<int>((m + 15) / 16);
-        const int tiles_n = static_cast<int>((n + 15) / 16);
-        const uint32_t* wq = reinterpret_cast<const uint32_t*>(w_packed);
-        const bool few = tiles_m * tiles_n <= dev.cu_count;
-        const bool stage = m > kSkinnyDirectMaxRows;
-        const int waves = few ? kSkinnyWavesFew : kSkinnyWavesMany;
-        auto kernel = few ? (stage ? q4_gemm_skinny_kernel<kSkinnyWavesFew, true>
-                                   : q4_gemm_skinny_kernel<kSkinnyWavesFew, false>)
-                          : (stage ? q4_gemm_skinny_kernel<kSkinnyWavesMany, true>
-                                   : q4_gemm_skinny_kernel<kSkinnyWavesMany, false>);
-        hipLaunchKernelGGL(kernel, dim3(tiles_m * tiles_n), dim3(64 * waves), 0, stream, x, wq, w_scales, y, mm,
-                           static_cast<int>(n), kk, tiles_m, tpart, plan.t_splits, lbp, rr, lora_scale);
-        return hipGetLastError();
-    }
-    if (plan.kind == Q4Plan::kSkinnySplitK) {
-        e = launch_mfma<1, 4, 1, 4, kSkinnyPD>(x, w_packed, w_scales, out, m, n, k, plan.splits, tpart, plan.t_splits,
-                                               lbp, rank, lora_scale, stream);
-    } else {
-        const int tiles_m = static_cast<int>((m + kWideTile - 1) / kWideTile);
-        const int tiles_n = static_cast<int>((n + kWideTile - 1) / kWideTile);
-        const int G = static_cast<int>(k / kGroup);
-        const int groups_per_split = (G + plan.splits - 1) / plan.splits;
-        hipLaunchKernelGGL(q4_gemm_wide_kernel, dim3(tiles_m * tiles_n, plan.splits),
-                           dim3(64 * kWideWavesPerTile), 0, stream, xs, reinterpret_cast<const uint32_t*>(w_packed),
-                           w_scales, out, mm, static_cast<int>(n), kk, tiles_m, tiles_n, groups_per_split, tpart,
-                           plan.t_splits, lbp, rr, lora_scale);
-        e = hipGetLastError();
-    }
+    const int tiles_m = static_cast<int>((m + kWideTile - 1) / kWideTile);
+    const int tiles_n = static_cast<int>((n + kWideTile - 1) / kWideTile);
+    const int G = static_cast<int>(k / kGroup);
+    const int groups_per_split = (G + plan.splits - 1) / plan.splits;
+    hipLaunchKernelGGL(q4_gemm_wide_kernel, dim3(tiles_m * tiles_n, plan.splits),
+                       dim3(64 * kWideWavesPerTile), 0, stream, xs, reinterpret_cast<const uint32_t*>(w_packed),
+                       w_scales, out, mm, static_cast<int>(n), kk, tiles_m, tiles_n, groups_per_split, tpart,
+                       plan.t_splits, lbp, rr, lora_scale);
+    const hipError_t e = hipGetLastError();
     if (e != hipSuccess || plan.splits == 1) return e;
     const size_t count = static_cast<size_t>(m) * n;
     size_t blocks = (count + 255) / 256;

@@ -1,27 +1,20 @@
-// Decode GEMV for 1..4 rows: y[m][n] = sum_k x[m][k] * v(k, n) * s(n, k/32).
+// Decode GEMV for one row: y[n] = sum_k x[k] * v(k, n) * s(n, k/32), K <= 4096.
 //
 // HBM-bound: one pass over the packed weights and scales. Work mapping:
-//   - a wavefront owns CPW consecutive columns; lane l owns the scale groups
-//     g = l, l + 64, ... of each. A column's packed bytes are contiguous
+//   - a wavefront owns a run of consecutive columns; lane l owns the scale groups
+//     g = l, l + 64 of each. A column's packed bytes are contiguous
 //     (q4gemm.comp:13, byte n*(K/2) + k/2), so for one column the 64 lanes'
 //     16-byte loads cover 1 KiB of contiguous memory: every weight load is a
 //     fully coalesced 128-bit load, and a lane's 16 bytes are exactly one
 //     32-value scale group. The lane's scale s(n, g) is one coalesced 32-bit
 //     load (lanes hold consecutive groups of the column), so no LDS broadcast
 //     is needed: each scale is read once, by the one lane that applies it;
-//   - all weight and scale loads of the wavefront's columns for a K chunk are
-//     issued before any arithmetic, so the whole wavefront's data is in flight
-//     at once; the columns are then consumed in issue order as they land;
-//   - x stays in registers for the whole chunk (the lane's own groups), read
-//     straight from global memory (it is tiny and L1/L2 resident);
-//   - nibbles are decoded in registers to v / 16 by v_cvt_off_f32_i4
-//     (nibbles_signed_16th, exact), so a group partial is 2^-4 * sum x v with
-//     no offset to cancel; it is scaled by s and accumulated per lane; the 64
-//     lane partials of a column are summed with DPP row operations plus two
-//     row broadcasts, and the factor 16 restored exactly at the end.
-// K larger than one chunk (64 * SPC groups per lane pass) is walked in chunks.
-// One row with K <= 4096 takes the software-pipelined integer kernel below
-// (q4_gemv_pipe_kernel), which reads the weights in the same mapping.
+//   - each group sum is formed exactly in integers (v_dot8_i32_i4 on x recoded
+//     as signed hex digits, below) and the group partials are accumulated and
+//     summed over the wavefront in double, so no fp32 rounding touches the sum.
+// Every other shape up to 32 rows (several rows, or K > 4096) is the small-batch
+// GEMM's (q4_small.hip), which forms its group sums the same exact way on the
+// int8 matrix cores.
 #include "q4_device.hpp"
 #include "q4_kernels.hpp"
 
@@ -35,176 +28,25 @@ __device__ __forceinline__ float dpp_src(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
 }
 
-// Sum over the 64 lanes; every lane receives the total (readlane of lane 63).
-__device__ __forceinline__ float wave_reduce_dpp(float v) {
+// The same DPP move of a double, one 32-bit half at a time (a row outside ROW_MASK reads 0).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ double dpp_src(double v) {
+    const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), CTRL, ROW_MASK, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), CTRL, ROW_MASK, 0xF, false);
+    return __hiloint2double(hi, lo);
+}
+
+// Sum over the 64 lanes in double; every lane receives the total (readlane of lane 63).
+__device__ __forceinline__ double wave_reduce_dpp(double v) {
     v += dpp_src<0xB1>(v);         // quad_perm [1,0,3,2]: pairs
     v += dpp_src<0x4E>(v);         // quad_perm [2,3,0,1]: quads
     v += dpp_src<0x141>(v);        // row_half_mirror: 8-lane halves
     v += dpp_src<0x140>(v);        // row_mirror: 16-lane rows
     v += dpp_src<0x142, 0xA>(v);   // row_bcast:15 into rows 1 and 3
     v += dpp_src<0x143, 0xC>(v);   // row_bcast:31 into rows 2 and 3 -> row 3 holds the total
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-
-// Loads of one K chunk for CPW columns: x first (coalesced, into xr), then every
-// weight and scale word. Kept in one straight-line block so the memory counters,
-// which retire loads in issue order, release x before any weight data.
-template <int M, int SPC, int CPW>
-struct ChunkLoads {
-    static constexpr int kChunkF4 = 64 * SPC * 8;  // float4 of x per row and chunk
-    static constexpr int kPerThread = kChunkF4 / kGemvThreads;
-    static_assert(kChunkF4 % kGemvThreads == 0, "x chunk must split evenly over the workgroup");
-    f32x4 xr[M][kPerThread];
-    u32x4 wv[CPW][SPC];
-    float sc[CPW][SPC];
-};
-
-template <int M, int SPC, int CPW>
-__device__ __forceinline__ void issue_chunk(ChunkLoads<M, SPC, CPW>& L, const float* x,
-                                            const u32x4* __restrict__ wq, const float* __restrict__ ws, int N,
-                                            int K, int G, int col0, int g0, int lane) {
-    using CL = ChunkLoads<M, SPC, CPW>;
-    const int c4_begin = g0 * 8;
-    const int c4_last = min(CL::kChunkF4, (K >> 2) - c4_begin) - 1;
-#pragma unroll
-    for (int m = 0; m < M; ++m)
-#pragma unroll
-        for (int i = 0; i < CL::kPerThread; ++i) {
-            // slots past K repeat the last chunk; their groups get a zero scale
-            const int c = min(static_cast<int>(threadIdx.x) + i * kGemvThreads, c4_last);
-            L.xr[m][i] = reinterpret_cast<const f32x4*>(x + static_cast<size_t>(m) * K)[c4_begin + c];
-        }
-    // Compiler-only fence: no load moves across it, so x is issued before the weights
-    // (x is deliberately not __restrict__, which would let its loads sink past it).
-    asm volatile("" ::: "memory");
-    // Column bases are wave-uniform (SGPR); the lane's offset is one unsigned 32-bit
-    // byte offset, so each load is SGPR base + VGPR offset.
-    uint32_t off16[SPC], off4[SPC];
-#pragma unroll
-    for (int s = 0; s < SPC; ++s) {
-        const uint32_t g = static_cast<uint32_t>(min(g0 + 64 * s + lane, G - 1));
-        off16[s] = g * 16u;
-        off4[s] = g * 4u;
-    }
-#pragma unroll
-    for (int c = 0; c < CPW; ++c) {
-        const size_t base = static_cast<size_t>(min(col0 + c, N - 1)) * G;
-        const char* wcol = reinterpret_cast<const char*>(wq + base);
-        const char* scol = reinterpret_cast<const char*>(ws + base);
-#pragma unroll
-        for (int s = 0; s < SPC; ++s) {
-            L.wv[c][s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wcol + off16[s]));
-            L.sc[c][s] = __builtin_nontemporal_load(reinterpret_cast<const float*>(scol + off4[s]));
-        }
-    }
-    asm volatile("" ::: "memory");
-}
-
-template <int M, int SPC, int CPW>
-__device__ __forceinline__ void consume_chunk(ChunkLoads<M, SPC, CPW>& L, f32x4* xs, float (&acc)[CPW][M], int G,
-                                              int g0, int lane) {
-    using CL = ChunkLoads<M, SPC, CPW>;
-    // x to LDS (chunk q of group g at slot g*8 + (q ^ (g & 7)): a wavefront's 128-bit
-    // reads of 64 groups then hit 8 distinct 16-byte bank groups per 8 lanes).
-#pragma unroll
-    for (int m = 0; m < M; ++m)
-#pragma unroll
-        for (int i = 0; i < CL::kPerThread; ++i) {
-            const int c = static_cast<int>(threadIdx.x) + i * kGemvThreads;
-            const int g = c >> 3, q = c & 7;
-            xs[m * CL::kChunkF4 + (g << 3) + (q ^ (g & 7))] = L.xr[m][i];
-        }
-    __syncthreads();
-    float xv[M][SPC][32];
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-#pragma unroll
-        for (int s = 0; s < SPC; ++s) {
-            const int gl = 64 * s + lane;
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const f32x4 t = xs[m * CL::kChunkF4 + (gl << 3) + (q ^ (gl & 7))];
-                xv[m][s][4 * q + 0] = t[0];
-                xv[m][s][4 * q + 1] = t[1];
-                xv[m][s][4 * q + 2] = t[2];
-                xv[m][s][4 * q + 3] = t[3];
-            }
-        }
-    }
-    // Groups past K contribute through a zero scale: a select, not a branch, so no
-    // branch splits the batch of outstanding loads.
-#pragma unroll
-    for (int c = 0; c < CPW; ++c)
-#pragma unroll
-        for (int s = 0; s < SPC; ++s) L.sc[c][s] = (g0 + 64 * s + lane < G) ? L.sc[c][s] : 0.0f;
-
-    // Columns in issue order, each as soon as its loads have landed.
-#pragma unroll
-    for (int c = 0; c < CPW; ++c) {
-#pragma unroll
-        for (int s = 0; s < SPC; ++s) {
-            float f[32];
-#pragma unroll
-            for (int w = 0; w < 4; ++w) nibbles_signed_16th(L.wv[c][s][w], *reinterpret_cast<float(*)[8]>(&f[8 * w]));
-#pragma unroll
-            for (int m = 0; m < M; ++m) {
-                float p0 = 0.0f, p1 = 0.0f;
-#pragma unroll
-                for (int k = 0; k < 16; ++k) {
-                    p0 = fmaf(xv[m][s][k], f[k], p0);
-                    p1 = fmaf(xv[m][s][16 + k], f[16 + k], p1);
-                }
-                acc[c][m] = fmaf(L.sc[c][s], p0 + p1, acc[c][m]);
-            }
-        }
-    }
-}
-
-// SINGLE: K fits one chunk (G <= 64 * SPC), straight-line code; otherwise K is
-// walked chunk by chunk.
-template <int M, int SPC, int CPW, bool SINGLE>
-__global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const float* x,  // not restrict: see issue_chunk
-                                                              const u32x4* __restrict__ wq,
-                                                              const float* __restrict__ ws,
-                                                              float* __restrict__ y, int N, int K) {
-    using CL = ChunkLoads<M, SPC, CPW>;
-    __shared__ f32x4 xs[M * CL::kChunkF4];
-    const int lane = threadIdx.x & 63;
-    // The wavefront index is uniform; readfirstlane keeps it and every column base
-    // derived from it in SGPRs. Every wavefront takes part in the barriers;
-    // past-the-end wavefronts work on a clamped column and store nothing.
-    const int wave =
-        __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x * (kGemvThreads >> 6) + (threadIdx.x >> 6)));
-    const int col0 = wave * CPW;
-    const int G = K >> 5;
-
-    float acc[CPW][M];
-#pragma unroll
-    for (int c = 0; c < CPW; ++c)
-#pragma unroll
-        for (int m = 0; m < M; ++m) acc[c][m] = 0.0f;
-
-    if constexpr (SINGLE) {
-        CL L;
-        issue_chunk<M, SPC, CPW>(L, x, wq, ws, N, K, G, col0, 0, lane);
-        consume_chunk<M, SPC, CPW>(L, xs, acc, G, 0, lane);
-    } else {
-        for (int g0 = 0; g0 < G; g0 += 64 * SPC) {
-            CL L;
-            issue_chunk<M, SPC, CPW>(L, x, wq, ws, N, K, G, col0, g0, lane);
-            if (g0 > 0) __syncthreads();  // previous chunk's LDS reads are done
-            consume_chunk<M, SPC, CPW>(L, xs, acc, G, g0, lane);
-        }
-    }
-#pragma unroll
-    for (int c = 0; c < CPW; ++c) {
-        const int col = col0 + c;
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-            const float total = wave_reduce_dpp(acc[c][m]);
-            if (lane == 0 && col < N) y[static_cast<size_t>(m) * N + col] = total * kSixteenthsUnit;
-        }
-    }
+    const int lo = __builtin_amdgcn_readlane(__double2loint(v), 63);
+    const int hi = __builtin_amdgcn_readlane(__double2hiint(v), 63);
+    return __hiloint2double(hi, lo);
 }
 
 // Software-pipelined single-row decode (M = 1, K <= 4096) in integer arithmetic.
@@ -224,9 +66,12 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const float* x,  
 //   sum_k v_k X_k = 65536 H + L,  H = sum_{j=4..7} 16^(j-4) sum_k v_k d_kj,
 //                                 L = sum_{j=0..3} 16^j     sum_k v_k d_kj,
 // both evaluated by Horner steps (a shift by 4 between digits). Over one group
-// |H|, |L| <= 32 * 8 * 34952 < 2^24, so both are exact in int32 and in float, and
-// 65536 H + L is rounded once (one fma). The group partial
-// (65536 H + L) * 2^(e_g - 30) * s(n, g) is accumulated in fp32 per lane.
+// |H|, |L| <= 32 * 8 * 34952 < 2^24, so both are exact in int32, and 65536 H + L is
+// exact in double. The group partial (65536 H + L) * 2^(e_g - 30) * s(n, g) is
+// accumulated in double per lane and the 64 lane partials are summed in double
+// (DPP), so the one rounding per group is double's: with fp32 accumulation the
+// reference KAT's ranges (x in [-1, 1), scales in [0.5, 1.5)) measured 2.1e-5 at
+// K = 1024 on outputs near zero, with double 6e-8 (the fp32 rounding of y itself).
 // Cost per 32 nibbles: 32 v_dot8 + 6 shifts + 6 other VALU ops, against 68 for
 // decoding to float (4 x (8 conversions + 1 shift + 8 fma)); the kernel is bound
 // by its per-wavefront VALU time as much as by HBM, so this is what buys speed.
@@ -282,6 +127,7 @@ template <int SPC>
 struct XDigits {
     uint32_t d[SPC][4 * kXDigits];
     float c[SPC];
+    double cd[SPC];  // c as double
 };
 
 // One column's weights and scales through buffer resources whose base is the
@@ -308,8 +154,8 @@ __device__ __forceinline__ void pipe_issue(PipeSlot<SPC>& slot, const u32x4* __r
 
 // The lane's share of one column (not yet summed over the wavefront).
 template <int SPC>
-__device__ __forceinline__ float pipe_partial(const PipeSlot<SPC>& slot, const XDigits<SPC>& xd) {
-    float acc = 0.0f;
+__device__ __forceinline__ double pipe_partial(const PipeSlot<SPC>& slot, const XDigits<SPC>& xd) {
+    double acc = 0.0;
 #pragma unroll
     for (int s = 0; s < SPC; ++s) {
         int hi = 0;
@@ -330,8 +176,8 @@ __device__ __forceinline__ float pipe_partial(const PipeSlot<SPC>& slot, const X
                 lo = __builtin_amdgcn_sdot8(static_cast<int>(slot.wv[s][w]), static_cast<int>(xd.d[s][w * kXDigits + j]),
                                             lo, false);
         }
-        const float p = fmaf(static_cast<float>(hi), 65536.0f, static_cast<float>(lo));
-        acc = fmaf(slot.sc[s], p * xd.c[s], acc);
+        const double p = fma(static_cast<double>(hi), 65536.0, static_cast<double>(lo));
+        acc = fma(p, static_cast<double>(slot.sc[s]) * xd.cd[s], acc);
     }
     return acc;
 }
@@ -364,7 +210,7 @@ __device__ __forceinline__ void pipe_ieee_columns(const float* x, const uint32_t
 }
 
 template <int SPC, int D>
-__global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float* x,  // not restrict: see issue_chunk
+__global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float* x,  // not restrict: x loads stay ahead of the weights
                                                                    const u32x4* __restrict__ wq,
                                                                    const float* __restrict__ ws,
                                                                    float* __restrict__ y, int N, int K, int reps) {
@@ -461,6 +307,7 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
             xd.d[s][4 * q + 3] = t[3];
         }
         xd.c[s] = xcs[gl];
+        xd.cd[s] = static_cast<double>(xd.c[s]);
     }
     // The wavefront's lanes cover every group of x, so this test is the same in every
     // wavefront of the grid (uniform): with a non-finite x the integer form has nothing to
@@ -486,7 +333,7 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
             const int i = r * S + s;
             pipe_issue<SPC>(slot[(s + D) % S], wq, ws, col0 + i + D, N, G, off16, off4);
             __builtin_amdgcn_sched_barrier(0);
-            const float t = wave_reduce_dpp(pipe_partial<SPC>(slot[s], xd));
+            const float t = static_cast<float>(wave_reduce_dpp(pipe_partial<SPC>(slot[s], xd)));
             result = lane == i ? t : result;
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -495,34 +342,11 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
 #pragma unroll
     for (int s = 0; s < D; ++s) {
         const int i = reps * S + s;
-        const float t = wave_reduce_dpp(pipe_partial<SPC>(slot[s], xd));
+        const float t = static_cast<float>(wave_reduce_dpp(pipe_partial<SPC>(slot[s], xd)));
         result = lane == i ? t : result;
     }
     // lane c holds column col0 + c: one coalesced store of the wavefront's run
     if (lane < cpb && col0 + lane < N) y[col0 + lane] = result;
-}
-
-template <int M, int SPC, int CPW>
-hipError_t launch_rows(const float* x, const uint8_t* w_packed, const float* w_scales, float* y, uint32_t n,
-                       uint32_t k, hipStream_t stream) {
-    const size_t waves = (static_cast<size_t>(n) + CPW - 1) / CPW;
-    const size_t blocks = (waves + kGemvThreads / 64 - 1) / (kGemvThreads / 64);
-    const bool single = (k / kGroup) <= static_cast<uint32_t>(64 * SPC);
-    // One row reaches this kernel only for K > 4096 (the pipelined kernel takes the rest),
-    // so its single-chunk form is never instantiated.
-    if constexpr (M > 1) {
-        if (single) {
-            hipLaunchKernelGGL((q4_gemv_kernel<M, SPC, CPW, true>), dim3(static_cast<unsigned>(blocks)),
-                               dim3(kGemvThreads), 0, stream, x, reinterpret_cast<const u32x4*>(w_packed), w_scales, y,
-                               static_cast<int>(n), static_cast<int>(k));
-            return hipGetLastError();
-        }
-    }
-    if (single) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((q4_gemv_kernel<M, SPC, CPW, false>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(kGemvThreads), 0, stream, x, reinterpret_cast<const u32x4*>(w_packed), w_scales, y,
-                       static_cast<int>(n), static_cast<int>(k));
-    return hipGetLastError();
 }
 
 }  // namespace
@@ -553,15 +377,8 @@ static hipError_t launch_gemv_pipelined(const DeviceInfo& dev, const float* x, c
 
 hipError_t launch_gemv(const DeviceInfo& dev, const float* x, const uint8_t* w_packed, const float* w_scales,
                        float* y, uint32_t m, uint32_t n, uint32_t k, hipStream_t stream) {
-    switch (m) {
-        case 1:
-            if (k / kGroup <= 128) return launch_gemv_pipelined(dev, x, w_packed, w_scales, y, n, k, stream);
-            return launch_rows<1, 2, 8>(x, w_packed, w_scales, y, n, k, stream);
-        case 2: return launch_rows<2, 2, 4>(x, w_packed, w_scales, y, n, k, stream);
-        case 3: return launch_rows<3, 1, 4>(x, w_packed, w_scales, y, n, k, stream);
-        case 4: return launch_rows<4, 1, 4>(x, w_packed, w_scales, y, n, k, stream);
-        default: return hipErrorInvalidValue;
-    }
+    if (m != 1 || k / kGroup > static_cast<uint32_t>(kGemvPipeMaxGroups)) return hipErrorInvalidValue;
+    return launch_gemv_pipelined(dev, x, w_packed, w_scales, y, n, k, stream);
 }
 
 }  // namespace spaceslug

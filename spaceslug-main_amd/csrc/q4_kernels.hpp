@@ -16,16 +16,17 @@ constexpr int kGroup = 32;
 // Largest LoRA rank of the fused epilogues (SPACESLUG_Q4_MAX_LORA_RANK in runtime_abi.h).
 constexpr int kMaxLoraRank = 64;
 
-// The decode GEMV handles 1..kGemvMaxRows rows; taller inputs go to the MFMA kernels.
-constexpr int kGemvMaxRows = 4;
+// The decode GEMV takes one row with K <= 32 * kGemvPipeMaxGroups; every other shape up to 32 rows
+// goes to the small-batch GEMM, taller ones to the wide and mid-size kernels.
+constexpr int kGemvPipeMaxGroups = 128;
 
 // Launch shape chosen by plan_q4gemm for one call.
 struct Q4Plan {
-    // kGemv: decode GEMV (m <= 4, no LoRA); kSkinny: m <= 32 with k % 128 == 0, K split
-    // inside the workgroup; kSkinnySplitK: other m <= 32; kWide: m > 32; kMid: m > 32 without
-    // LoRA whose 128 x 128 grid would need a K-split while its 64 x 64 grid fits the CUs once
-    // (k % 64 == 0, k <= 4096).
-    enum Kind { kGemv, kSkinny, kSkinnySplitK, kWide, kMid } kind;
+    // kGemv: one-row decode GEMV (k <= 4096, no LoRA); kDigits: every other call up to 32 rows,
+    // exact integer group sums on the int8 matrix cores (q4_small.hip); kWide: m > 32; kMid:
+    // m > 32 without LoRA whose 128 x 128 grid would need a K-split while its 64 x 64 grid fits
+    // the CUs once (k % 64 == 0, k <= 4096).
+    enum Kind { kGemv, kDigits, kWide, kMid } kind;
     int splits;              // K-splits of the MFMA kernel (1 = write y directly)
     size_t workspace_bytes;  // device scratch the call needs (split partials, LoRA T partials and T, x limbs)
     int t_splits;            // K-splits of the LoRA pre-pass T = x * lora_a (0 without LoRA)
@@ -39,7 +40,7 @@ struct DeviceInfo {
 // Decides the kernel and K-split for (m, n, k, rank). rank == 0 means no LoRA.
 Q4Plan plan_q4gemm(const DeviceInfo& dev, uint32_t m, uint32_t n, uint32_t k, uint32_t rank);
 
-// Decode GEMV, 1 <= m <= kGemvMaxRows (no LDS, no device memory beyond its arguments).
+// Decode GEMV, m == 1 and k <= 32 * kGemvPipeMaxGroups (no device memory beyond its arguments).
 hipError_t launch_gemv(const DeviceInfo& dev, const float* x, const uint8_t* w_packed,
                        const float* w_scales, float* y, uint32_t m, uint32_t n, uint32_t k,
                        hipStream_t stream);
@@ -50,6 +51,16 @@ hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float*
                          const uint8_t* w_packed, const float* w_scales, float* y, uint32_t m,
                          uint32_t n, uint32_t k, const float* la, const float* lb, uint32_t rank,
                          float lora_scale, void* workspace, hipStream_t stream);
+
+// Workspace of the small-batch GEMM (kDigits) before any LoRA T partials: x as four int8 digits per
+// value in MFMA lane order plus one exponent per (row, group).
+size_t digits_workspace_bytes(uint32_t m, uint32_t k);
+
+// Small-batch GEMM (kDigits): one preparation launch (x digits, LoRA T partials) and the GEMM.
+// `workspace` holds digits_workspace_bytes(m, k) bytes, then t_splits * m * rank floats of T partials.
+hipError_t launch_q4gemm_digits(const DeviceInfo& dev, const float* x, const uint8_t* w_packed, const float* w_scales,
+                                float* y, uint32_t m, uint32_t n, uint32_t k, const float* la, const float* lb,
+                                uint32_t rank, float lora_scale, int t_splits, void* workspace, hipStream_t stream);
 
 // Bytes of the wide int4 GEMM's x limbs for x (fp32, m x k, k % 32 == 0): three exact bf16 limbs
 // per value in 16-row blocks (rows padded with zeros to a multiple of 16), written by the

@@ -435,15 +435,16 @@ def test_lora_m512_k4096_n4096_r16(session, oracle, gpu):
     assert torch.equal(y_t, base)
 
 
-def test_capture_of_workspace_call_is_refused(session, oracle, gpu):
-    """A call that needs the library's shared workspace (m > 32 here) returns -4 while its stream is being
-    captured, before touching the workspace, and the capture still ends cleanly; the same call outside
-    capture then succeeds."""
+@pytest.mark.parametrize("m", [64, 16])
+def test_capture_of_workspace_call_is_refused(session, oracle, gpu, m):
+    """A call that needs the library's shared workspace (the x limbs above 32 rows, the x digits of the
+    small-batch GEMM) returns -4 while its stream is being captured, before touching the workspace, and
+    the capture still ends cleanly; the same call outside capture then succeeds."""
     import ctypes
 
     import torch
 
-    m, n, k = 64, 256, 256
+    n, k = 256, 256
     note(f"capture refusal m={m} n={n} k={k}")
     c = make_case(m, n, k)
     x_t, w_t, s_t = to_dev(c.x, torch), to_dev(c.packed, torch), to_dev(c.scales, torch)
@@ -503,14 +504,16 @@ def test_split_k_calls_on_two_streams(session, oracle, gpu, m, n, k):
         check(oracle, ys[i].cpu().numpy(), want[i], label=f"stream {i}")
 
 
-@pytest.mark.parametrize("m", [1, 16])
-def test_projection_chain_in_a_hip_graph(session, oracle, gpu, m):
-    """Two chained projections (y1 = x W1, y2 = y1 W2) captured once in a HIP graph through the device entry
-    point and replayed with new inputs: every replay equals the eager chain bit for bit. Shapes that need no
-    library workspace (decode GEMV, small-M kernel) are capturable."""
+@pytest.mark.parametrize("m,entry", [(1, "device"), (16, "noalloc")])
+def test_projection_chain_in_a_hip_graph(session, oracle, gpu, m, entry):
+    """Two chained projections (y1 = x W1, y2 = y1 W2) captured once in a HIP graph and replayed with new
+    inputs: every replay equals the eager chain bit for bit. The one-row decode GEMV needs no library
+    workspace, so the device entry point captures it; a 16-row call needs the x digits' workspace, so it
+    is captured through the entry point that allocates nothing (its fixed scratch)."""
     import torch
 
-    note(f"graph chain m={m}")
+    note(f"graph chain m={m} entry={entry}")
+    call = session.q4gemm_device if entry == "device" else session.q4gemm_device_noalloc
     k1, n1, n2 = 512, 1024, 384
     c1 = make_case(m, n1, k1, seed_b=0x51, seed_s=0x52)
     c2 = make_case(m, n2, n1, seed_b=0x61, seed_s=0x62)
@@ -521,8 +524,8 @@ def test_projection_chain_in_a_hip_graph(session, oracle, gpu, m):
     y2 = torch.empty((m, n2), dtype=torch.float32, device="cuda:0")
 
     def chain(stream):
-        session.q4gemm_device(x.data_ptr(), w1.data_ptr(), s1.data_ptr(), y1.data_ptr(), m, n1, k1, stream)
-        session.q4gemm_device(y1.data_ptr(), w2.data_ptr(), s2.data_ptr(), y2.data_ptr(), m, n2, n1, stream)
+        call(x.data_ptr(), w1.data_ptr(), s1.data_ptr(), y1.data_ptr(), m, n1, k1, stream)
+        call(y1.data_ptr(), w2.data_ptr(), s2.data_ptr(), y2.data_ptr(), m, n2, n1, stream)
 
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
