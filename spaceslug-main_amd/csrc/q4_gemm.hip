@@ -860,7 +860,7 @@ Q4Plan plan_q4gemm(const DeviceInfo& dev, uint32_t m, uint32_t n, uint32_t k, ui
     }
     if (m <= 32) {
         plan.kind = Q4Plan::kDigits;
-        plan.workspace_bytes = align_up(digits_workspace_bytes(m, k)) + lora_bytes;
+        plan.workspace_bytes = lora_bytes;  // the T partials of a LoRA call; none otherwise
         return plan;
     }
     plan.kind = Q4Plan::kWide;
@@ -896,8 +896,8 @@ hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float*
                          float lora_scale, void* workspace, hipStream_t stream) {
     if (plan.kind == Q4Plan::kGemv) return launch_gemv(dev, x, w_packed, w_scales, y, m, n, k, stream);
     if (plan.kind == Q4Plan::kDigits)
-        return launch_q4gemm_digits(dev, x, w_packed, w_scales, y, m, n, k, la, lb, rank, lora_scale, plan.t_splits,
-                                    workspace, stream);
+        return launch_q4gemm_small(dev, x, w_packed, w_scales, y, m, n, k, la, lb, rank, lora_scale, plan.t_splits,
+                                   workspace, stream);
     if (plan.kind == Q4Plan::kMid) {
         uint16_t* xs = static_cast<uint16_t*>(workspace);
         const int tiles_m = static_cast<int>((m + kMidTile - 1) / kMidTile);

@@ -52,15 +52,11 @@ hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float*
                          uint32_t n, uint32_t k, const float* la, const float* lb, uint32_t rank,
                          float lora_scale, void* workspace, hipStream_t stream);
 
-// Workspace of the small-batch GEMM (kDigits) before any LoRA T partials: x as four int8 digits per
-// value in MFMA lane order plus one exponent per (row, group).
-size_t digits_workspace_bytes(uint32_t m, uint32_t k);
-
-// Small-batch GEMM (kDigits): one preparation launch (x digits, LoRA T partials) and the GEMM.
-// `workspace` holds digits_workspace_bytes(m, k) bytes, then t_splits * m * rank floats of T partials.
-hipError_t launch_q4gemm_digits(const DeviceInfo& dev, const float* x, const uint8_t* w_packed, const float* w_scales,
-                                float* y, uint32_t m, uint32_t n, uint32_t k, const float* la, const float* lb,
-                                uint32_t rank, float lora_scale, int t_splits, void* workspace, hipStream_t stream);
+// Small-batch GEMM (kDigits, q4_small.hip): one launch, plus a preparation launch for the LoRA T
+// partials; `workspace` holds t_splits * m * rank floats of them (unused without LoRA).
+hipError_t launch_q4gemm_small(const DeviceInfo& dev, const float* x, const uint8_t* w_packed, const float* w_scales,
+                               float* y, uint32_t m, uint32_t n, uint32_t k, const float* la, const float* lb,
+                               uint32_t rank, float lora_scale, int t_splits, void* workspace, hipStream_t stream);
 
 // Bytes of the wide int4 GEMM's x limbs for x (fp32, m x k, k % 32 == 0): three exact bf16 limbs
 // per value in 16-row blocks (rows padded with zeros to a multiple of 16), written by the
