@@ -20,13 +20,13 @@
 // Work mapping: a workgroup owns 8 rows x 32 columns (one MFMA tile; lane l of the result
 // holds column l % 32, rows 2i + l / 32 for i < 4) and its wavefronts split K; their float64
 // accumulators are summed through LDS in wavefront order (deterministic). Per wavefront, x,
-// packed weights and scales reach LDS by buffer loads to LDS in chunks of 4 groups, two
-// chunks in flight; lane (row r, half h, quarter q) recodes 4 values of a group and the
-// digits reach the MFMA lanes through a 1 KiB LDS exchange.
+// packed weights and scales reach LDS by buffer loads to LDS in chunks of 4 groups, three
+// chunks in flight; lane (row r, half h, quarter q) recodes 4 values of a group and writes
+// the digits over the group's 1 KiB of staged x, in the layout the MFMA lanes read.
 // Rows holding an infinity or a NaN are flagged while recoding and their outputs formed in
 // IEEE double arithmetic over the non-finite terms, which is the double reference's result
 // for such rows (test_q4gemm.cpp:102-119).
-#include <climits>
+#include <type_traits>
 
 #include "q4_device.hpp"
 #include "q4_kernels.hpp"
@@ -35,6 +35,7 @@
 namespace spaceslug {
 namespace {
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void* lds_ptr;
@@ -43,15 +44,13 @@ constexpr int kDigitRows = 8;        // rows of x per MFMA row block (x 4 digits
 constexpr int kDigitCols = 32;       // columns per MFMA tile
 constexpr int kDigitFracBits = 30;   // |X| <= 2^30
 constexpr uint32_t kDigitBias = 0x80808080u;
-constexpr int kExpNonFinite = INT_MIN;
-constexpr int kChunk = 4;            // groups per staged chunk
-constexpr int kXBytes = kChunk * kDigitRows * 128;  // x of a chunk: [group][row][32 floats] (4 KiB)
-constexpr int kBBytes = kDigitCols * kChunk * 16;   // packed weights (2 KiB)
-constexpr int kSBytes = kDigitCols * kChunk * 4;    // scales (512 B)
+constexpr int kChunk = 2;            // groups per staged chunk
+constexpr int kXBytes = kChunk * kDigitRows * 128;  // x of a chunk: [group][row][32 floats] (2 KiB)
+constexpr int kBBytes = kDigitCols * kChunk * 16;   // packed weights: [column][2 groups][16 B] (1 KiB)
+constexpr int kSBytes = kDigitCols * kChunk * 4;    // scales: [column][2 groups] (256 B)
 constexpr int kBOff = kXBytes, kSOff = kBOff + kBBytes;
 constexpr int kStageBytes = kSOff + kSBytes;
-constexpr int kXchgBytes = kChunk * 64 * 16;        // digit exchange of a chunk's groups
-constexpr int kExpBytes = kChunk * kDigitRows * 4;  // exponents of a chunk's groups
+constexpr int kStages = 3;           // chunks in flight per wavefront
 constexpr int kBufferWord3 = 0x00020000;            // buffer resource word 3: 32-bit data format
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, size_t bytes) {
@@ -68,7 +67,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, si
 template <int BYTES>
 __device__ __forceinline__ void copy_to_lds(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset, uint32_t soffset,
                                             unsigned char* lds) {
-    const uint32_t l = (uint32_t)(size_t)(lds_ptr)lds;  // the LDS address
+    // the LDS address and the scalar offset are wavefront-uniform; readfirstlane states it
+    const uint32_t l = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(lds_ptr)lds);
+    soffset = __builtin_amdgcn_readfirstlane(soffset);
     uint32_t saved;
     if constexpr (BYTES == 16)
         asm volatile(
@@ -86,16 +87,28 @@ __device__ __forceinline__ void copy_to_lds(__amdgpu_buffer_rsrc_t rsrc, uint32_
             : "memory");
 }
 
-// 4 x 4 byte transpose: byte i of o[d] = byte d of in[i].
-__device__ __forceinline__ void transpose_bytes(uint32_t a, uint32_t b, uint32_t c, uint32_t e, uint32_t (&o)[4]) {
-    const uint32_t t0 = __builtin_amdgcn_perm(b, a, 0x06020400u);  // a0 b0 a2 b2
-    const uint32_t t1 = __builtin_amdgcn_perm(b, a, 0x07030501u);  // a1 b1 a3 b3
-    const uint32_t t2 = __builtin_amdgcn_perm(e, c, 0x06020400u);  // c0 e0 c2 e2
-    const uint32_t t3 = __builtin_amdgcn_perm(e, c, 0x07030501u);  // c1 e1 c3 e3
-    o[0] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);              // a0 b0 c0 e0
-    o[1] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);              // a1 b1 c1 e1
-    o[2] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);              // a2 b2 c2 e2
-    o[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);              // a3 b3 c3 e3
+// Byte selectors of a 4 x 4 byte transpose whose outputs come in the order s ^ r.
+struct TransposeSel {
+    uint32_t even, odd, lo, hi;
+    __device__ explicit TransposeSel(int r)
+        : even((r & 1) ? 0x07030501u : 0x06020400u), odd((r & 1) ? 0x06020400u : 0x07030501u),
+          lo((r & 2) ? 0x07060302u : 0x05040100u), hi((r & 2) ? 0x05040100u : 0x07060302u) {}
+};
+
+// 4 x 4 byte transpose: byte i of o[s] = byte s ^ r of in[i]. With r = 0 the first level pairs
+// bytes 0, 2 (even) and 1, 3 (odd) of a, b and of c, e, the second joins the low or high halves:
+// o[0] = a0 b0 c0 e0, o[1] = a1 b1 c1 e1, ...; odd r swaps the first level's roles, r >= 2 the
+// second's.
+__device__ __forceinline__ void transpose_bytes(uint32_t a, uint32_t b, uint32_t c, uint32_t e,
+                                                const TransposeSel& sel, uint32_t (&o)[4]) {
+    const uint32_t t0 = __builtin_amdgcn_perm(b, a, sel.even);
+    const uint32_t t1 = __builtin_amdgcn_perm(b, a, sel.odd);
+    const uint32_t t2 = __builtin_amdgcn_perm(e, c, sel.even);
+    const uint32_t t3 = __builtin_amdgcn_perm(e, c, sel.odd);
+    o[0] = __builtin_amdgcn_perm(t2, t0, sel.lo);
+    o[1] = __builtin_amdgcn_perm(t3, t1, sel.lo);
+    o[2] = __builtin_amdgcn_perm(t2, t0, sel.hi);
+    o[3] = __builtin_amdgcn_perm(t3, t1, sel.hi);
 }
 
 // K slot order shared by the A (digits) and B (weights) operands: in the 16 bytes a lane feeds
@@ -110,6 +123,14 @@ __device__ __forceinline__ i32x4 weights_i8x16(uint32_t w0, uint32_t w1) {
 // Exponent slot of local row ml within a group: [h = ml & 1][i = ml >> 1], so the lanes of
 // result half h read their four rows 2 i + h as one 16-byte word.
 __device__ __forceinline__ int exp_slot(int ml) { return (ml & 1) * 4 + (ml >> 1); }
+
+// Nearest integer of v, halves rounded up (floor(v + 0.5) in one conversion, exact for every float);
+// an infinity or a NaN converts to a clamped value without trapping. |v| <= 2^30 here.
+__device__ __forceinline__ int round_half_up(float v) {
+    int r;
+    asm("v_cvt_rpi_i32_f32 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
 
 // LoRA preparation launch of a small-batch call: the T partials only (lora_t_block).
 __global__ __launch_bounds__(256) void small_lora_prep_kernel(const float* __restrict__ x, const float* __restrict__ la,
@@ -139,19 +160,20 @@ __device__ float ieee_row_value(const float* x, const uint32_t* wq, const float*
 }
 
 // NI: output register pairs per lane in use (rows 2 i + h, i < NI): 1 for M <= 2, 2 for M <= 4,
-// else 4. W: wavefronts per workgroup, splitting K.
+// else 4. W: wavefronts per workgroup, splitting K. Every variant keeps four wavefronts per SIMD
+// resident (at most 128 VGPRs and 40 KiB of LDS per wavefront), which hides the recoding's
+// dependent chains.
 template <int NI, int W>
-__global__ __launch_bounds__(64 * W) void q4_gemm_small_kernel(const float* x, const uint32_t* wq, const float* ws,
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))) void q4_gemm_small_kernel(const float* x, const uint32_t* wq, const float* ws,
                                                                float* __restrict__ y, int M, int N, int K, int RB,
                                                                int tiles_n, const float* __restrict__ tpart,
                                                                int t_splits, const float* __restrict__ lb, int R,
                                                                float lscale) {
-    __shared__ __align__(16) unsigned char stage0[W * kStageBytes];
-    __shared__ __align__(16) unsigned char stage1[W * kStageBytes];
-    __shared__ __align__(16) unsigned char xchg[W * (kXchgBytes + kExpBytes)];
+    __shared__ __align__(16) unsigned char stages[kStages * W * kStageBytes];
+    __shared__ __align__(16) int exps[W * kChunk * kDigitRows];
     __shared__ int rowmask;
-    static_assert(W * NI * 64 * 8 <= W * kStageBytes, "epilogue partials fit stage0");
-    static_assert((kDigitRows + kDigitCols) * kMaxLoraRank * 4 <= W * kStageBytes, "LoRA staging fits stage1");
+    static_assert(W * NI * 64 * 8 <= W * kStageBytes, "epilogue partials fit stage 0");
+    static_assert((kDigitRows + kDigitCols) * kMaxLoraRank * 4 <= W * kStageBytes, "LoRA staging fits stage 1");
     const int lane = static_cast<int>(threadIdx.x) & 63;
     const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int c = lane & 31;  // result column of this lane
@@ -170,50 +192,48 @@ __global__ __launch_bounds__(64 * W) void q4_gemm_small_kernel(const float* x, c
     if (threadIdx.x == 0) rowmask = 0;
     __syncthreads();
 
-    // This wavefront's groups [gb, ge), in chunks of kChunk.
-    const int gpw = (G + W - 1) / W;
-    const int gb = min(G, w * gpw);
-    const int ge = min(G, gb + gpw);
-    const int nchunks = (ge - gb + kChunk - 1) / kChunk;
+    // The workgroup's K range in chunks of kChunk groups, dealt to its wavefronts in turn (wave w
+    // takes chunks w, w + W, ...): at any moment the wavefronts read neighbouring chunks, so each
+    // column's weights are read as one run rather than W scattered pieces.
+    const int nct = (G + kChunk - 1) / kChunk;
+    const int nchunks = nct > w ? (nct - w + W - 1) / W : 0;
+    auto chunk_group = [&](int j) { return (w + j * W) * kChunk; };
 
     // Every copy goes through a buffer resource with a uniform base: the lane's part is a fixed
     // 32-bit offset and the chunk's position a scalar offset, so issuing costs no vector ALU work,
     // and a read past a resource's end returns zeros (rows past M, columns past N).
     //   x: instruction gi moves group gi of the chunk for the block's 8 rows (lane i: row i / 8,
     //   16 bytes at i % 8), one 128-byte run per row.
-    //   Weights: instruction p moves columns 16p .. 16p+15 of the tile, 64 bytes (the chunk's 4
-    //   groups) each; lane i takes column 16p + i / 4 and group slot (i % 4) ^ f(column),
-    //   f(c) = (c >> 2) & 3, so that the MFMA-side reads (lane (c, h) reads one group of column c)
-    //   hit 16 distinct 16-byte bank groups per 16 lanes.
-    //   Scales: instruction p moves the 4 scales of the same columns.
+    //   Weights: one instruction moves the tile's 32 columns, 32 bytes (the chunk's 2 groups)
+    //   each; lane i takes column i / 2 and group slot (i % 2) ^ f(column), f(c) = (c >> 3) & 1,
+    //   so that the MFMA-side reads (lane (c, h) reads group h of column c) hit 16 distinct
+    //   16-byte bank groups per 16 lanes.
+    //   Scales: one instruction moves the 2 scales of each column, lane i column i / 2.
     const __amdgpu_buffer_rsrc_t rx =
         make_rsrc(x + static_cast<size_t>(m0) * K, static_cast<size_t>(M - m0) * K * 4);
-    const uint32_t vx = static_cast<uint32_t>((lane >> 3) * K * 4 + (lane & 7) * 16);
-    const int ci = lane >> 2;
-    const int gs = lane & 3;
-    __amdgpu_buffer_rsrc_t rw[2], rs[2];
-    uint32_t vw[2], vs[2];
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-        const int col0 = min(n0 + 16 * p, N);
-        const size_t left = static_cast<size_t>(N - col0) * G;
-        rw[p] = make_rsrc(wq + static_cast<size_t>(col0) * G * 4, left * 16);
-        rs[p] = make_rsrc(ws + static_cast<size_t>(col0) * G, left * 4);
-        vw[p] = static_cast<uint32_t>((ci * G + (gs ^ (((16 * p + ci) >> 2) & 3))) * 16);
-        vs[p] = static_cast<uint32_t>((ci * G + gs) * 4);
-    }
-    const int fsw = (c >> 2) & 3;  // swizzle of this lane's column
+    // x placement: the 16-byte unit at slot q of row r's 128 bytes holds the row's unit
+    // q ^ xsw(r), xsw(r) = (r >> 1) & 1, so that the recoding reads below (rows 0-3 and 4-7 in
+    // the two halves of the wavefront, even or odd units per instruction) meet distinct banks.
+    const uint32_t vx = static_cast<uint32_t>((lane >> 3) * K * 4 + ((lane & 7) ^ ((lane >> 4) & 1)) * 16);
+    const int ci = lane >> 1;
+    const int gs = lane & 1;
+    const size_t left = static_cast<size_t>(N - n0) * G;
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(wq + static_cast<size_t>(n0) * G * 4, left * 16);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(ws + static_cast<size_t>(n0) * G, left * 4);
+    const uint32_t vw = static_cast<uint32_t>((ci * G + (gs ^ ((ci >> 3) & 1))) * 16);
+    const uint32_t vs = static_cast<uint32_t>((ci * G + gs) * 4);
+    const int bsw = (c >> 3) & 1;  // swizzle of this lane's column
 
-    // The 8 copies of a chunk (counted by the waits below).
-    constexpr int kCopiesPerChunk = kChunk + 2 + 2;
-    auto issue = [&](int cb, unsigned char* st) {
+    // A chunk's copies: x (kChunk of them), then weights and scales (2).
+    static_assert(kChunk == 2, "copy counts and the partial chunk assume two groups per chunk");
+    auto issue_x = [&](int cb, unsigned char* st) {
 #pragma unroll
         for (int gi = 0; gi < kChunk; ++gi)
             copy_to_lds<16>(rx, vx, static_cast<uint32_t>((cb + gi) * 128), st + gi * 1024);
-#pragma unroll
-        for (int p = 0; p < 2; ++p) copy_to_lds<16>(rw[p], vw[p], static_cast<uint32_t>(cb * 16), st + kBOff + p * 1024);
-#pragma unroll
-        for (int p = 0; p < 2; ++p) copy_to_lds<4>(rs[p], vs[p], static_cast<uint32_t>(cb * 4), st + kSOff + p * 256);
+    };
+    auto issue_ws = [&](int cb, unsigned char* st) {
+        copy_to_lds<16>(rw, vw, static_cast<uint32_t>(cb * 16), st + kBOff);
+        copy_to_lds<4>(rs, vs, static_cast<uint32_t>(cb * 4), st + kSOff);
     };
 
     // Recoding roles: lane (row rr = lane / 8, half rh = (lane / 4) % 2, quarter rq = lane % 4)
@@ -221,48 +241,82 @@ __global__ __launch_bounds__(64 * W) void q4_gemm_small_kernel(const float* x, c
     // (rq & 1) + 2 i, so its byte-transposed digits are exactly dword rq of the four A lanes
     // (row rr, digit d, half rh); the 8 lanes of a row hold its whole group.
     const int rr = lane >> 3, rh = (lane >> 2) & 1, rq = lane & 3;
-    const int xoff = rr * 128 + rh * 64 + (rq >> 1) * 32 + (rq & 1) * 4;
-    unsigned char* xg = xchg + w * (kXchgBytes + kExpBytes);
-    int* xexp = reinterpret_cast<int*>(xg + kXchgBytes);
+    const int xq0 = 4 * rh + 2 * (rq >> 1), xsw = (rr >> 1) & 1;  // units xq0, xq0 + 1 of the row
+    const int xoff0 = rr * 128 + (xq0 ^ xsw) * 16 + (rq & 1) * 4;
+    const int xoff1 = rr * 128 + ((xq0 + 1) ^ xsw) * 16 + (rq & 1) * 4;
+    // Digit writes: lane (row rr, half rh, quarter rq) writes digit d to dword rq of A lane
+    // 32 rh + 4 rr + d. Its four writes go out in the order s ^ dr, dr = 2 rh + rr / 4, so that
+    // each write instruction meets 64 distinct banks.
+    const TransposeSel tsel(2 * rh + (rr >> 2));
+    int wofs[4];
+#pragma unroll
+    for (int sl = 0; sl < 4; ++sl) wofs[sl] = ((32 * rh + 4 * rr + (sl ^ (2 * rh + (rr >> 2)))) * 4 + rq) * 4;
+    int* xexp = exps + w * kChunk * kDigitRows;
 
     double acc[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) acc[i] = 0.0;
 
-    // Recodes group gi of the chunk in stage st into exchange slot gi; the group's exponents
-    // (e - 34, or INT_MIN with a non-finite value) go to xexp[gi][exp_slot(row)].
-    auto recode = [&](const unsigned char* st, int gi) {
-        const float* xs = reinterpret_cast<const float*>(st + gi * 1024 + xoff);
-        const float v0 = xs[0], v1 = xs[2], v2 = xs[4], v3 = xs[6];
-        // largest magnitude as an integer maximum of the sign-cleared bits: every non-finite value
-        // (0x7F800000 and above) also lands at the top, so one compare detects it; the row's 8
-        // lanes combine theirs (quad pairs, then the two quads)
-        uint32_t mb = max(max(__float_as_uint(v0) & 0x7FFFFFFFu, __float_as_uint(v1) & 0x7FFFFFFFu),
-                          max(__float_as_uint(v2) & 0x7FFFFFFFu, __float_as_uint(v3) & 0x7FFFFFFFu));
-        mb = max(mb, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mb), 0xB1, 0xF, 0xF, false)));
-        mb = max(mb, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mb), 0x4E, 0xF, 0xF, false)));
-        mb = max(mb, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mb), 0x141, 0xF, 0xF, false)));
-        const bool finite = mb < 0x7F800000u;
-        int e = 0;
-        (void)frexpf(__uint_as_float(mb), &e);  // max < 2^e (e = 0 for an all-zero group)
-        const int sh = kDigitFracBits - e;
-        uint32_t z[4];
-        const float vv[4] = {v0, v1, v2, v3};
+    // Recodes groups g0 .. g0 + NG - 1 of the chunk in stage st, in phases over the groups so that
+    // their chains interleave: each group's digits are written over its x (a wavefront's LDS
+    // operations run in order, so every lane's reads of a group precede the writes) and its
+    // exponents (e - 34) go to xexp[group][exp_slot(row)]. Branch-free; a non-finite value only
+    // raises mbrun, the lane's largest magnitude bits, which flags its row once the loop is done
+    // (its digits and exponents are then never used).
+    uint32_t mbrun = 0;
+    auto recode = [&](const unsigned char* st, int g0, auto ng) {
+        constexpr int NG = decltype(ng)::value;
+        float vv[NG][4];
+        uint32_t mb[NG];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int X = finite ? static_cast<int>(rintf(ldexpf(vv[i], sh))) : 0;
-            z[i] = (static_cast<uint32_t>(X) + kDigitBias) ^ kDigitBias;  // byte d = signed digit D_d
+        for (int g = 0; g < NG; ++g) {
+            const float* xs0 = reinterpret_cast<const float*>(st + (g0 + g) * 1024 + xoff0);
+            const float* xs1 = reinterpret_cast<const float*>(st + (g0 + g) * 1024 + xoff1);
+            vv[g][0] = xs0[0];
+            vv[g][1] = xs0[2];
+            vv[g][2] = xs1[0];
+            vv[g][3] = xs1[2];
         }
-        uint32_t t[4];
-        transpose_bytes(z[0], z[1], z[2], z[3], t);  // t[d]: digit d of the 4 values = dword rq
-        int* xw = reinterpret_cast<int*>(xg + gi * 1024);
+        // largest magnitude as an integer maximum of the sign-cleared bits (every non-finite value,
+        // 0x7F800000 and above, lands at the top); the row's 8 lanes combine theirs (quad pairs,
+        // then the two quads)
 #pragma unroll
-        for (int d = 0; d < 4; ++d) xw[(32 * rh + 4 * rr + d) * 4 + rq] = static_cast<int>(t[d]);
-        if ((lane & 7) == 0) xexp[gi * 8 + exp_slot(rr)] = finite ? e - 34 : kExpNonFinite;
-        if (!finite) atomicOr(&rowmask, 1 << rr);  // rare: a row with an infinity or a NaN
+        for (int g = 0; g < NG; ++g)
+            mb[g] = max(max(__float_as_uint(vv[g][0]) & 0x7FFFFFFFu, __float_as_uint(vv[g][1]) & 0x7FFFFFFFu),
+                        max(__float_as_uint(vv[g][2]) & 0x7FFFFFFFu, __float_as_uint(vv[g][3]) & 0x7FFFFFFFu));
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+            mb[g] = max(mb[g], static_cast<uint32_t>(
+                                   __builtin_amdgcn_update_dpp(0, static_cast<int>(mb[g]), 0xB1, 0xF, 0xF, false)));
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+            mb[g] = max(mb[g], static_cast<uint32_t>(
+                                   __builtin_amdgcn_update_dpp(0, static_cast<int>(mb[g]), 0x4E, 0xF, 0xF, false)));
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+            mb[g] = max(mb[g], static_cast<uint32_t>(
+                                   __builtin_amdgcn_update_dpp(0, static_cast<int>(mb[g]), 0x141, 0xF, 0xF, false)));
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            mbrun = max(mbrun, mb[g]);
+            const int e = __builtin_amdgcn_frexp_expf(__uint_as_float(mb[g]));  // max < 2^e (0: all-zero group)
+            const int sh = kDigitFracBits - e;
+            uint32_t z[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                z[i] = (static_cast<uint32_t>(round_half_up(ldexpf(vv[g][i], sh))) + kDigitBias) ^ kDigitBias;
+            uint32_t t[4];
+            transpose_bytes(z[0], z[1], z[2], z[3], tsel, t);  // t[sl]: digit sl ^ dr of the 4 values
+            unsigned char* xw = const_cast<unsigned char*>(st) + (g0 + g) * 1024;
+#pragma unroll
+            for (int sl = 0; sl < 4; ++sl) *reinterpret_cast<uint32_t*>(xw + wofs[sl]) = t[sl];
+            xexp[(g0 + g) * 8 + exp_slot(rr)] = e - 34;  // the row's 8 lanes store the same value
+        }
     };
     // A lane (row, digit, half) = lane 32 half + 4 row + digit reads its 16 bytes of group gi.
-    auto digits = [&](int gi) { return *reinterpret_cast<const i32x4*>(xg + gi * 1024 + lane * 16); };
+    auto digits = [&](const unsigned char* st, int gi) {
+        return *reinterpret_cast<const i32x4*>(st + gi * 1024 + lane * 16);
+    };
 
     auto fold = [&](const i32x16& r, float sf, const i32x4& e4) {
         const double sd = static_cast<double>(sf);
@@ -275,81 +329,73 @@ __global__ __launch_bounds__(64 * W) void q4_gemm_small_kernel(const float* x, c
         }
     };
 
-    auto compute = [&](int cb, const unsigned char* st) {
-        const f32x4 s4 = *reinterpret_cast<const f32x4*>(st + kSOff + c * 16);
-        // B operands: lane (c, 0) reads group 2p, lane (c, 1) group 2p + 1, and the swaps leave
-        // lane (c, h) with packed words 2h and 2h + 1 of both groups.
-        i32x4 bq[kChunk];
-#pragma unroll
-        for (int p = 0; p < kChunk / 2; ++p) {
-            const u32x4 wv = *reinterpret_cast<const u32x4*>(st + kBOff + 64 * c + 16 * ((2 * p + h) ^ fsw));
-            const auto x0 = __builtin_amdgcn_permlane32_swap(wv[0], wv[2], false, false);
-            const auto x1 = __builtin_amdgcn_permlane32_swap(wv[1], wv[3], false, false);
-            bq[2 * p] = weights_i8x16(x0[0], x1[0]);
-            bq[2 * p + 1] = weights_i8x16(x0[1], x1[1]);
-        }
+    // Recodes the chunk at group cb (its groups in the K range) in stage st.
+    auto recode_chunk = [&](int cb, const unsigned char* st) {
+        if (G - cb >= kChunk)
+            recode(st, 0, std::integral_constant<int, kChunk>{});
+        else
+            recode(st, 0, std::integral_constant<int, 1>{});
+    };
+    // The chunk's MFMAs and folds; the MFMA of group 1 is issued before group 0's fold.
+    auto mfma_chunk = [&](int cb, const unsigned char* st) {
+        const f32x2 s2 = *reinterpret_cast<const f32x2*>(st + kSOff + c * 8);
+        // B operands: lane (c, 0) reads group 0, lane (c, 1) group 1, and the swaps leave lane
+        // (c, h) with packed words 2h and 2h + 1 of both groups.
+        const u32x4 wv = *reinterpret_cast<const u32x4*>(st + kBOff + 32 * c + 16 * (h ^ bsw));
+        const auto x0 = __builtin_amdgcn_permlane32_swap(wv[0], wv[2], false, false);
+        const auto x1 = __builtin_amdgcn_permlane32_swap(wv[1], wv[3], false, false);
         const i32x16 zero = {};
-        const int valid = ge - cb;  // groups of this chunk in the wavefront's range (uniform)
-        if (valid >= kChunk) {
-            // Full chunk, straight-line: the four groups are recoded back to back (independent
-            // chains), then the MFMA of group g + 1 is issued before group g's fold.
-#pragma unroll
-            for (int g = 0; g < kChunk; ++g) recode(st, g);
-            i32x4 a[kChunk], e4[kChunk];
-#pragma unroll
-            for (int g = 0; g < kChunk; ++g) {
-                a[g] = digits(g);
-                e4[g] = *reinterpret_cast<const i32x4*>(xexp + g * 8 + h * 4);
-            }
-            i32x16 r = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0], bq[0], zero, 0, 0, 0);
-#pragma unroll
-            for (int g = 0; g < kChunk; ++g) {
-                i32x16 rn;
-                if (g + 1 < kChunk) rn = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[g + 1], bq[g + 1], zero, 0, 0, 0);
-                fold(r, s4[g], e4[g]);
-                if (g + 1 < kChunk) r = rn;
-            }
+        const i32x4 a0 = digits(st, 0);
+        const i32x4 e0 = *reinterpret_cast<const i32x4*>(xexp + h * 4);
+        const i32x16 r0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, weights_i8x16(x0[0], x1[0]), zero, 0, 0, 0);
+        if (G - cb >= kChunk) {
+            const i32x4 a1 = digits(st, 1);
+            const i32x4 e1 = *reinterpret_cast<const i32x4*>(xexp + 8 + h * 4);
+            const i32x16 r1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, weights_i8x16(x0[1], x1[1]), zero, 0, 0, 0);
+            fold(r0, s2[0], e0);
+            fold(r1, s2[1], e1);
         } else {
-#pragma unroll
-            for (int g = 0; g < kChunk; ++g) {
-                if (g < valid) {
-                    recode(st, g);
-                    const i32x16 r = __builtin_amdgcn_mfma_i32_32x32x32_i8(digits(g), bq[g], zero, 0, 0, 0);
-                    fold(r, s4[g], *reinterpret_cast<const i32x4*>(xexp + g * 8 + h * 4));
-                }
-            }
+            fold(r0, s2[0], e0);
         }
     };
 
-    // Two stages: chunk j in stage j % 2. Chunk j + 1's copies are issued before chunk j is
-    // computed; copies retire in issue order, so leaving exactly those in flight is chunk j's wait.
-    unsigned char* st0 = stage0 + w * kStageBytes;
-    unsigned char* st1 = stage1 + w * kStageBytes;
-    if (nchunks > 0) issue(gb, st0);
-    for (int j = 0; j < nchunks; j += 2) {
-        const int cb = gb + j * kChunk;
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // stage 1's previous reads are done
-        if (j + 1 < nchunks) {
-            issue(cb + kChunk, st1);
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kCopiesPerChunk) : "memory");
-        } else {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        }
-        compute(cb, st0);
-        if (j + 1 >= nchunks) break;
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // stage 0's reads are done
+    // Chunk j is staged in stage j % 3 of this wavefront and its copies are issued two chunks
+    // ahead, so up to three chunks are in flight. Copies retire in issue order: leaving the copies
+    // of the chunks issued after chunk j in flight is chunk j's wait. The loop is unrolled by the
+    // stage count so that every LDS address is a fixed offset from the wavefront's stages.
+    constexpr int kCopiesPerChunk = kChunk + 2;
+    unsigned char* wst = stages + w * kStages * kStageBytes;
+    auto issue = [&](int j, unsigned char* st) {
+        issue_x(chunk_group(j), st);
+        issue_ws(chunk_group(j), st);
+    };
+    auto step = [&](int j, unsigned char* st, unsigned char* st_ahead) {
         if (j + 2 < nchunks) {
-            issue(cb + 2 * kChunk, st0);
+            // the stage of chunk j + 2 last held chunk j - 1: its reads and digit writes are done
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            issue(j + 2, st_ahead);
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * kCopiesPerChunk) : "memory");
+        } else if (j + 1 < nchunks) {
             asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kCopiesPerChunk) : "memory");
         } else {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         }
-        compute(cb + kChunk, st1);
+        const int cb = chunk_group(j);
+        recode_chunk(cb, st);
+        mfma_chunk(cb, st);
+    };
+    if (nchunks > 0) issue(0, wst);
+    if (nchunks > 1) issue(1, wst + kStageBytes);
+    for (int j = 0; j < nchunks; j += kStages) {
+        step(j, wst, wst + 2 * kStageBytes);
+        if (j + 1 < nchunks) step(j + 1, wst + kStageBytes, wst);
+        if (j + 2 < nchunks) step(j + 2, wst + 2 * kStageBytes, wst + kStageBytes);
     }
 
+    if (mbrun >= 0x7F800000u) atomicOr(&rowmask, 1 << rr);  // rare: a row with an infinity or a NaN
     __syncthreads();  // every wavefront's K range is done: the stages are free
-    double* red = reinterpret_cast<double*>(stage0);
-    float* lora_t_s = reinterpret_cast<float*>(stage1);  // [8 rows][R]
+    double* red = reinterpret_cast<double*>(stages);
+    float* lora_t_s = reinterpret_cast<float*>(stages + W * kStageBytes);  // [8 rows][R]
     float* lora_b_s = lora_t_s + kDigitRows * kMaxLoraRank;  // [R][32 columns]
 #pragma unroll
     for (int i = 0; i < NI; ++i) red[(w * NI + i) * 64 + lane] = acc[i];
@@ -411,22 +457,24 @@ hipError_t launch_q4gemm_small(const DeviceInfo& dev, const float* x, const uint
         if (pe != hipSuccess) return pe;
     }
     const int tiles_n = (N + kDigitCols - 1) / kDigitCols;
-    const bool few = RB * tiles_n <= dev.cu_count;  // one round of workgroups: more wavefronts per tile
+    // Wavefronts per workgroup: 16 per CU in total, whether one, two or four workgroups share a CU.
+    const int total = RB * tiles_n;
+    const int W = total <= dev.cu_count ? 16 : total <= 2 * dev.cu_count ? 8 : 4;
+    const int NI = M <= 2 ? 1 : M <= 4 ? 2 : 4;
     const float* lbp = rank ? lb : nullptr;
-    if (M <= 2)
-        return few ? launch_small_gemm<1, 8>(x, w_packed, w_scales, y, M, N, K, RB, tiles_n, tpart, t_splits, lbp, R,
-                                             lora_scale, stream)
-                   : launch_small_gemm<1, 4>(x, w_packed, w_scales, y, M, N, K, RB, tiles_n, tpart, t_splits, lbp, R,
-                                             lora_scale, stream);
-    if (M <= 4)
-        return few ? launch_small_gemm<2, 8>(x, w_packed, w_scales, y, M, N, K, RB, tiles_n, tpart, t_splits, lbp, R,
-                                             lora_scale, stream)
-                   : launch_small_gemm<2, 4>(x, w_packed, w_scales, y, M, N, K, RB, tiles_n, tpart, t_splits, lbp, R,
-                                             lora_scale, stream);
-    return few ? launch_small_gemm<4, 8>(x, w_packed, w_scales, y, M, N, K, RB, tiles_n, tpart, t_splits, lbp, R,
-                                         lora_scale, stream)
-               : launch_small_gemm<4, 4>(x, w_packed, w_scales, y, M, N, K, RB, tiles_n, tpart, t_splits, lbp, R,
-                                         lora_scale, stream);
+    auto go = [&](auto ni, auto wv) {
+        return launch_small_gemm<decltype(ni)::value, decltype(wv)::value>(x, w_packed, w_scales, y, M, N, K, RB,
+                                                                           tiles_n, tpart, t_splits, lbp, R,
+                                                                           lora_scale, stream);
+    };
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I4 = std::integral_constant<int, 4>;
+    using W16 = std::integral_constant<int, 16>;
+    using W8 = std::integral_constant<int, 8>;
+    if (NI == 1) return W == 16 ? go(I1{}, W16{}) : W == 8 ? go(I1{}, W8{}) : go(I1{}, I4{});
+    if (NI == 2) return W == 16 ? go(I2{}, W16{}) : W == 8 ? go(I2{}, W8{}) : go(I2{}, I4{});
+    return W == 16 ? go(I4{}, W16{}) : W == 8 ? go(I4{}, W8{}) : go(I4{}, I4{});
 }
 
 }  // namespace spaceslug
