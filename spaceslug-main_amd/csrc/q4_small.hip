@@ -6,7 +6,7 @@
 // partials of a preparation launch):
 //   - each wavefront recodes the groups of x it consumes, per row and 32-value group, in
 //     31-bit fixed point: X = rint(x * 2^(30 - e)) with 2^(e-1) <= max|x| < 2^e over the
-//     group (|X| <= 2^30; error at most 2^-31 of the group's largest |x|), written as four
+//     group (|X| <= 2^30; error at most 2^(e - 31), i.e. 2^-30 of the group's largest |x|), written as four
 //     signed base-256 digits D_0..D_3 (X = sum_d 256^d D_d, each D_d in [-128, 127]: the bytes
 //     of (X + 0x80808080) xor 0x80808080);
 //   - v_mfma_i32_32x32x32_i8 takes one 32-value group per instruction: its 32 A rows are

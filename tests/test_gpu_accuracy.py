@@ -7,7 +7,7 @@ zero are held to an absolute 1e-5 by the metric |gpu - ref| / max(1, |ref|) (tes
 
 Up to 32 rows every path forms each group sum exactly in integers (the one-row decode GEMV with
 v_dot8 on hex digits of x, the small-batch GEMM with int8 MFMAs on byte digits of x) and sums the
-groups in double. The only approximation left is x's 31-bit fixed point per group (at most 2^-31 of
+groups in double. The only approximation left is x's 31-bit fixed point per group (at most 2^-30 of
 the group's largest |x| per value), so these cases are held to 2e-7: a few fp32 roundings of y
 itself. An fp32 group sum measured 2e-5 to 8e-5 on the same inputs, so a return of one fails here.
 

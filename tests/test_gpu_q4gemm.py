@@ -105,11 +105,14 @@ def test_gemv_one_row_column_runs(session, oracle, gpu, n):
     check(oracle, got, oracle.q4gemm_packed(c.x, c.packed, c.scales, threads=threads()), label=f"gemv n={n}")
 
 
-@pytest.mark.parametrize("m,n,k", [(8, 5000, 512), (9, 4096, 512), (24, 700, 2048), (32, 4096, 1024), (31, 1000, 640)])
-def test_small_m_both_x_paths(session, oracle, gpu, m, n, k):
-    """M <= 32 with K % 128 == 0: x loaded straight into registers (M <= 8) or copied through
-    LDS first (M > 8), each with 16 wavefronts per tile (tile grid fits the CUs) and with 8
-    (it does not: 8x5000, 32x4096), on ragged row tiles (24, 31) and K of 4 to 16 quads."""
+@pytest.mark.parametrize("m,n,k", [(8, 5000, 512), (9, 4096, 512), (24, 700, 2048), (32, 4096, 1024), (31, 1000, 640),
+                                   (2, 9000, 512), (32, 8192, 256), (4, 20000, 256), (17, 14336, 512)])
+def test_small_m_grid_shapes(session, oracle, gpu, m, n, k):
+    """The small-batch digit kernel (M <= 32) in each of its launch forms: 16 wavefronts per
+    8-row x 32-column tile when the tile grid fits the CUs (8x5000, 9x4096, 24x700, 31x1000), 8
+    when it fits twice (32x4096, 2x9000) and 4 beyond (32x8192, 4x20000, 17x14336); one, two or
+    four result rows per lane in use (M <= 2, <= 4, more); ragged row blocks (9, 17, 24, 31 rows)
+    and ragged column tiles."""
     note(f"small-m m={m} n={n} k={k}")
     c = make_case(m, n, k)
     got = session.q4gemm_values(c.x, c.packed, c.scales, m, n, k)
@@ -213,15 +216,17 @@ def test_one_row_x_groups_of_very_different_magnitude(session, oracle, gpu, k):
     check(oracle, got, oracle.q4gemm_packed(x, c.packed, c.scales, threads=threads()), label="x magnitudes")
 
 
-@pytest.mark.parametrize("m,k", [(2, 4096), (24, 512)])
-def test_float_paths_x_groups_of_very_different_magnitude(session, oracle, gpu, m, k):
-    """The same groups on the multi-row paths, which form products in fp32, without the 1e30
-    group: there, cancellation among terms of that size is rounded at 2^-24 of the terms, as in
-    any fp32 GEMM, and can exceed 1e-5 of the (much smaller) result."""
-    note(f"x group magnitudes m={m} k={k}")
+@pytest.mark.parametrize("m,k,huge", [(2, 4096, True), (24, 512, True), (40, 512, False)])
+def test_multi_row_x_groups_of_very_different_magnitude(session, oracle, gpu, m, k, huge):
+    """The same groups on the multi-row paths. Up to 32 rows (2, 24) the digit kernel sums each
+    group exactly, so the 1e30 group is included as on the one-row kernel. Above 32 rows (40) the
+    bf16-limb kernel rounds each group sum in fp32, without the 1e30 group: there, cancellation
+    among terms of that size is rounded at 2^-24 of the terms, as in any fp32 GEMM, and can exceed
+    1e-5 of the (much smaller) result."""
+    note(f"x group magnitudes m={m} k={k} huge={huge}")
     n = 300
     c = make_case(m, n, k)
-    x = magnitude_stress_x(c.x, huge=False)
+    x = magnitude_stress_x(c.x, huge=huge)
     got = session.q4gemm_values(x, c.packed, c.scales, m, n, k)
     check(oracle, got, oracle.q4gemm_packed(x, c.packed, c.scales, threads=threads()), label="x magnitudes")
 
@@ -241,11 +246,12 @@ def test_nan_in_x_gives_nan_outputs(session, oracle, gpu, m):
         check(oracle, got[1:], oracle.q4gemm_packed(x[1:], c.packed, c.scales), label="rows without nan")
 
 
-@pytest.mark.parametrize("m,k", [(1, 512), (1, 8192), (3, 512), (24, 512), (24, 544), (64, 512)])
+@pytest.mark.parametrize("m,k", [(1, 512), (1, 8192), (3, 512), (24, 512), (24, 544), (64, 512), (64, 544)])
 def test_nonfinite_x_matches_reference_pattern(session, oracle, gpu, m, k):
-    """Infinities and NaNs in x on every path: the integer GEMV (1 x 512), the float GEMV
-    (1 x 8192, 3 rows), the in-workgroup K split (24 x 512), the K-split kernel (24 x 544) and
-    the wide bf16-limb kernel (64 rows). Every output of a row holding a non-finite value is
+    """Infinities and NaNs in x on every path: the integer GEMV (1 x 512), the small-batch digit
+    kernel (1 x 8192, 3 and 24 rows), the mid-size bf16-limb kernel (64 x 512) and the wide
+    bf16-limb kernel with a K split and its reduction launch (64 x 544: K % 64 != 0 keeps it off
+    the mid-size kernel). Every output of a row holding a non-finite value is
     non-finite, NaN exactly where the double reference has NaN (inf * 0, opposite infinities,
     a NaN) and the same signed infinity elsewhere; rows without one meet the usual bar."""
     note(f"non-finite x m={m} k={k}")

@@ -56,8 +56,9 @@ def test_noalloc_matches_workspace_entry(runtime_lib_path, oracle, gpu):
 
     L = _lib(runtime_lib_path)
     # first a K-split wide call (x limbs and split partials in the scratch: 28 MiB), then a smaller
-    # one whose split partials land on what the first call left there
-    for m, n, k in ((512, 4096, 4096), (40, 300, 1056), (16, 512, 512)):
+    # one whose split partials land on what the first call left there, then a mid-size call (64 x 64
+    # whole-K tiles: x limbs by rows in the scratch) and a small-batch one (no scratch)
+    for m, n, k in ((512, 4096, 4096), (40, 300, 1056), (100, 301, 512), (16, 512, 512)):
         note(f"noalloc {m}x{n}x{k}")
         c = make_case(m, n, k, seed_a=0x12345678 + m, seed_b=0x9ABCDEF0 + n)
         x = torch.from_numpy(c.x).to("cuda:0")
