@@ -24,7 +24,7 @@
 //     blockIdx.y and a second kernel sums the partials in a fixed order.
 // LoRA: the preparation launch that splits x into limbs also computes T = x * la on
 // the MFMA as a few K-split partials (one per 1024 values of K), and the GEMM
-// epilogue sums them (lora_t_value) and adds scale * T[rows] * lb[:, cols] with the
+// epilogue sums them (lora_t_values) and adds scale * T[rows] * lb[:, cols] with the
 // same MFMA tile layout (r in the K slot) before the single store of y.
 #include <algorithm>
 #include <utility>
@@ -446,26 +446,56 @@ __global__ __launch_bounds__(512) void q4_gemm_wide_kernel(const uint16_t* xs, c
         float* ts = reinterpret_cast<float*>(&lds.a[0][0][0][0]);  // [128][RP]
         float* bs = ts + 128 * RP;                                  // [R][128]
         __syncthreads();  // every wavefront is past its last LDS read and copy
-        for (int e = tid; e < 128 * R; e += 512) {
-            const int row = e / R, r = e - row * R;
-            ts[row * RP + r] = lora_t_value(tpart, t_splits, M, R, min(mt0 + row, M - 1), r);
-            bs[e] = lb[static_cast<size_t>(e >> 7) * N + min(nt0 + (e & 127), N - 1)];
+        // Four values of T and of lb per thread and pass, every load of a pass issued before the
+        // first store (one load after another cost ~7 us per call at 512 x 4096 x 4096, r = 16).
+        constexpr int kNV = 4;
+        for (int e0 = tid; e0 < 128 * R; e0 += 512 * kNV) {
+            float tv[kNV], bv[kNV];
+#pragma unroll
+            for (int v = 0; v < kNV; ++v) {
+                const int e = e0 + 512 * v;
+                bv[v] = lb[static_cast<size_t>(min(e >> 7, R - 1)) * N + min(nt0 + (e & 127), N - 1)];  // in bounds
+            }
+            lora_t_values<kNV>(tpart, t_splits, M, R, mt0, e0, 512, 128 * R, tv);
+#pragma unroll
+            for (int v = 0; v < kNV; ++v) {
+                const int e = e0 + 512 * v;
+                if (e < 128 * R) {
+                    const int row = e / R, r = e - row * R;
+                    ts[row * RP + r] = tv[v];
+                    bs[e] = bv[v];
+                }
+            }
         }
         __syncthreads();
         const double s = static_cast<double>(lscale) * 0.0625;
+        // Eight ranks per pass: every operand of the pass read (unconditionally, at a rank clamped
+        // into range) before its MFMAs, which run the two 32-column tiles' chains interleaved; a
+        // rank past R enters as zeros.
+        f32x16 P[2] = {zero16, zero16};
+        for (int r8 = 0; r8 < R; r8 += 8) {
+            float av[4], bv[4][2];
 #pragma unroll
-        for (int tn = 0; tn < 2; ++tn) {
-            const int col_t = wn * 64 + 32 * tn + col32;
-            f32x16 P = zero16;
-            for (int r0 = 0; r0 < R; r0 += 2) {
-                const int r = r0 + half;
-                const float av = r < R ? ts[arow * RP + r] : 0.0f;
-                const float bv = r < R ? bs[r * 128 + col_t] : 0.0f;
-                P = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, P, 0, 0, 0);
+            for (int j = 0; j < 4; ++j) {
+                const int r = r8 + 2 * j + half, rc = min(r, R - 1);
+                const float a = ts[arow * RP + rc];
+                av[j] = r < R ? a : 0.0f;
+#pragma unroll
+                for (int tn = 0; tn < 2; ++tn) {
+                    const float b = bs[rc * 128 + wn * 64 + 32 * tn + col32];
+                    bv[j][tn] = r < R ? b : 0.0f;
+                }
             }
 #pragma unroll
-            for (int v = 0; v < 16; ++v) acc[tn][v] = fma(s, static_cast<double>(P[v]), acc[tn][v]);
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int tn = 0; tn < 2; ++tn)
+                    P[tn] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[j], bv[j][tn], P[tn], 0, 0, 0);
         }
+#pragma unroll
+        for (int tn = 0; tn < 2; ++tn)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[tn][v] = fma(s, static_cast<double>(P[tn][v]), acc[tn][v]);
     }
 
     float* dst = out + static_cast<size_t>(blockIdx.y) * M * N;

@@ -9,12 +9,41 @@
 namespace spaceslug {
 namespace {
 
-// T[row][r] = the sum of its t_splits partials, in double and in split order, rounded once.
-__device__ __forceinline__ float lora_t_value(const float* __restrict__ tpart, int t_splits, int M, int R, int row,
-                                              int r) {
-    double t = 0.0;
-    for (int z = 0; z < t_splits; ++z) t += static_cast<double>(tpart[(static_cast<size_t>(z) * M + row) * R + r]);
-    return static_cast<float>(t);
+// NV values of T for a GEMM epilogue: value v is element e = e0 + stride * v of the row-major
+// block [rows][R] whose first row is row0 (rows past M - 1 clamped to it), the sum of its t_splits
+// partials in double and in split order, rounded once; for e >= count it is a value the caller
+// drops. The loads of four partials of all NV values issue before the first of their sums: the
+// epilogue waits for one round of loads per four splits, not for one load after another.
+template <int NV>
+__device__ __forceinline__ void lora_t_values(const float* __restrict__ tpart, int t_splits, int M, int R, int row0,
+                                              int e0, int stride, int count, float (&out)[NV]) {
+    size_t idx[NV];
+    double t[NV];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+        const int e = min(e0 + stride * v, count - 1);
+        idx[v] = static_cast<size_t>(min(row0 + e / R, M - 1)) * R + e % R;
+        t[v] = 0.0;
+    }
+    // Every load unconditional and in bounds (the row clamped, a split past the last one re-reading
+    // the last): a load under a branch would be waited for where the branch joins.
+    const size_t plane = static_cast<size_t>(M) * R;
+    for (int z0 = 0; z0 < t_splits; z0 += 4) {
+        float p[4][NV];
+#pragma unroll
+        for (int dz = 0; dz < 4; ++dz) {
+            const size_t zo = static_cast<size_t>(min(z0 + dz, t_splits - 1)) * plane;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) p[dz][v] = tpart[zo + idx[v]];
+        }
+#pragma unroll
+        for (int dz = 0; dz < 4; ++dz)
+            if (z0 + dz < t_splits)
+#pragma unroll
+                for (int v = 0; v < NV; ++v) t[v] += static_cast<double>(p[dz][v]);
+    }
+#pragma unroll
+    for (int v = 0; v < NV; ++v) out[v] = static_cast<float>(t[v]);
 }
 
 // LoRA pre-pass on the MFMA: tpart[z][m][r] = sum over the kLoraGroupsPerBlock groups
@@ -22,7 +51,7 @@ __device__ __forceinline__ float lora_t_value(const float* __restrict__ tpart, i
 // wavefronts per 16 x 16 tile of (rows, ranks) and split; each wavefront takes
 // kLoraGroupsPerWave groups with all of its operands loaded before its first MFMA,
 // and the four sums are added through LDS in wavefront order. The GEMM epilogues
-// add the t_splits partials of T (lora_t_value), so T needs no reduction launch.
+// add the t_splits partials of T (lora_t_values), so T needs no reduction launch.
 constexpr int kLoraGroupsPerWave = 8;
 constexpr int kLoraGroupsPerBlock = 4 * kLoraGroupsPerWave;
 

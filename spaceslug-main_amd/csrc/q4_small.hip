@@ -400,10 +400,23 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))) voi
 #pragma unroll
     for (int i = 0; i < NI; ++i) red[(w * NI + i) * 64 + lane] = acc[i];
     if (lb != nullptr) {
-        for (int e = static_cast<int>(threadIdx.x); e < kDigitRows * R; e += 64 * W)
-            lora_t_s[e] = lora_t_value(tpart, t_splits, M, R, min(m0 + e / R, M - 1), e % R);
-        for (int e = static_cast<int>(threadIdx.x); e < R * kDigitCols; e += 64 * W)
-            lora_b_s[e] = lb[static_cast<size_t>(e >> 5) * N + min(n0 + (e & 31), N - 1)];
+        // T (8 rows) and lb (32 columns): every load of a pass issued before the first store.
+        constexpr int kNV = 2;
+        for (int e0 = static_cast<int>(threadIdx.x); e0 < R * kDigitCols; e0 += 64 * W * kNV) {
+            float tv[kNV], bv[kNV];
+#pragma unroll
+            for (int v = 0; v < kNV; ++v) {
+                const int e = e0 + 64 * W * v;
+                bv[v] = lb[static_cast<size_t>(min(e >> 5, R - 1)) * N + min(n0 + (e & 31), N - 1)];  // in bounds
+            }
+            lora_t_values<kNV>(tpart, t_splits, M, R, m0, e0, 64 * W, kDigitRows * R, tv);
+#pragma unroll
+            for (int v = 0; v < kNV; ++v) {
+                const int e = e0 + 64 * W * v;
+                if (e < kDigitRows * R) lora_t_s[e] = tv[v];
+                if (e < R * kDigitCols) lora_b_s[e] = bv[v];
+            }
+        }
     }
     __syncthreads();
     const int t = static_cast<int>(threadIdx.x);
@@ -420,6 +433,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))) voi
             if ((rowmask >> ml) & 1) s = ieee_row_value(x, wq, ws, m, n, K);
             if (lb != nullptr) {
                 double tb = 0.0;
+#pragma unroll 8
                 for (int r = 0; r < R; ++r)
                     tb = fma(static_cast<double>(lora_t_s[ml * R + r]), static_cast<double>(lora_b_s[r * 32 + cc]), tb);
                 s = fma(static_cast<double>(lscale), tb, s);
