@@ -23,7 +23,7 @@
 //     tiles take the shape if they fill the CUs once, else K is split across
 //     blockIdx.y and a second kernel sums the partials in a fixed order.
 // LoRA: the preparation launch that splits x into limbs also computes T = x * la on
-// the MFMA as a few K-split partials (one per 1024 values of K), and the GEMM
+// the MFMA as a few K-split partials (one per 512 values of K), and the GEMM
 // epilogue sums them (lora_t_values) and adds scale * T[rows] * lb[:, cols] with the
 // same MFMA tile layout (r in the K slot) before the single store of y.
 #include <algorithm>

@@ -12,8 +12,9 @@ namespace {
 // NV values of T for a GEMM epilogue: value v is element e = e0 + stride * v of the row-major
 // block [rows][R] whose first row is row0 (rows past M - 1 clamped to it), the sum of its t_splits
 // partials in double and in split order, rounded once; for e >= count it is a value the caller
-// drops. The loads of four partials of all NV values issue before the first of their sums: the
-// epilogue waits for one round of loads per four splits, not for one load after another.
+// drops. The loads of kLoraTRound partials of all NV values issue before the first of their sums:
+// the epilogue waits for one round of loads per kLoraTRound splits, not for one load after another.
+constexpr int kLoraTRound = 8;
 template <int NV>
 __device__ __forceinline__ void lora_t_values(const float* __restrict__ tpart, int t_splits, int M, int R, int row0,
                                               int e0, int stride, int count, float (&out)[NV]) {
@@ -28,16 +29,16 @@ __device__ __forceinline__ void lora_t_values(const float* __restrict__ tpart, i
     // Every load unconditional and in bounds (the row clamped, a split past the last one re-reading
     // the last): a load under a branch would be waited for where the branch joins.
     const size_t plane = static_cast<size_t>(M) * R;
-    for (int z0 = 0; z0 < t_splits; z0 += 4) {
-        float p[4][NV];
+    for (int z0 = 0; z0 < t_splits; z0 += kLoraTRound) {
+        float p[kLoraTRound][NV];
 #pragma unroll
-        for (int dz = 0; dz < 4; ++dz) {
+        for (int dz = 0; dz < kLoraTRound; ++dz) {
             const size_t zo = static_cast<size_t>(min(z0 + dz, t_splits - 1)) * plane;
 #pragma unroll
             for (int v = 0; v < NV; ++v) p[dz][v] = tpart[zo + idx[v]];
         }
 #pragma unroll
-        for (int dz = 0; dz < 4; ++dz)
+        for (int dz = 0; dz < kLoraTRound; ++dz)
             if (z0 + dz < t_splits)
 #pragma unroll
                 for (int v = 0; v < NV; ++v) t[v] += static_cast<double>(p[dz][v]);
@@ -52,7 +53,7 @@ __device__ __forceinline__ void lora_t_values(const float* __restrict__ tpart, i
 // kLoraGroupsPerWave groups with all of its operands loaded before its first MFMA,
 // and the four sums are added through LDS in wavefront order. The GEMM epilogues
 // add the t_splits partials of T (lora_t_values), so T needs no reduction launch.
-constexpr int kLoraGroupsPerWave = 8;
+constexpr int kLoraGroupsPerWave = 4;
 constexpr int kLoraGroupsPerBlock = 4 * kLoraGroupsPerWave;
 
 __device__ __forceinline__ void lora_t_block(const float* __restrict__ x, const float* __restrict__ la,
