@@ -303,8 +303,12 @@ def test_deterministic_repeat(session, oracle, gpu):
         assert np.array_equal(a, b)
 
 
+# The T partials cover 512 values of K each and an epilogue sums them eight at a time: K = 8192 (16
+# partials, two rounds), 4640 (10: a round of 8 and one of 2) and 1056 (3, the last one group) take
+# those paths, on both sides of 32 rows and up to rank 64.
 @pytest.mark.parametrize("m,n,k,rank", [(1, 64, 64, 4), (3, 100, 96, 1), (64, 64, 64, 8), (40, 200, 256, 16),
-                                        (130, 96, 512, 17), (16, 128, 128, 64)])
+                                        (130, 96, 512, 17), (16, 128, 128, 64), (40, 96, 8192, 16),
+                                        (5, 64, 4640, 9), (200, 130, 1056, 64), (32, 72, 8192, 64)])
 def test_lora_shapes(session, oracle, gpu, m, n, k, rank):
     note(f"lora m={m} n={n} k={k} r={rank}")
     c = make_case(m, n, k)
