@@ -435,33 +435,39 @@ __global__ __launch_bounds__(512) void q4_gemm_wide_kernel(const uint16_t* xs, c
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
 
-    if (lb != nullptr && blockIdx.y == 0) {
+    // LoRA ranks of this K-split: split z of S adds ranks [R z / S, R (z + 1) / S) (all of them
+    // without a split), so the splits share the term's loads and MFMAs.
+    const int r_lo = R * static_cast<int>(blockIdx.y) / static_cast<int>(gridDim.y);
+    const int nr = R * static_cast<int>(blockIdx.y + 1) / static_cast<int>(gridDim.y) - r_lo;
+    if (lb != nullptr && nr > 0) {  // uniform
         // LoRA term on the fp32 MFMA (r in the K slot), added as (lscale / 16) * P since the sums
         // are multiplied by 16 at the store. The stage buffers are free now: the tile's 128 rows
-        // of T (its partials summed) and 128 columns of lb are loaded there by the whole
-        // workgroup at once, rows padded to R + 1 floats, then read as MFMA operands.
+        // of T (its partials summed) and 128 columns of lb, for this split's nr ranks, are loaded
+        // there by the whole workgroup at once, rows padded to nr + 1 floats, then read as MFMA
+        // operands.
         static_assert(sizeof(lds.a) >= sizeof(float) * (128 * (kMaxLoraRank + 1) + kMaxLoraRank * 128),
                       "the LoRA tiles fit in the stage buffers");
-        const int RP = R + 1;
+        const int RP = nr + 1;
         float* ts = reinterpret_cast<float*>(&lds.a[0][0][0][0]);  // [128][RP]
-        float* bs = ts + 128 * RP;                                  // [R][128]
+        float* bs = ts + 128 * RP;                                  // [nr][128]
         __syncthreads();  // every wavefront is past its last LDS read and copy
         // Four values of T and of lb per thread and pass, every load of a pass issued before the
-        // first store (one load after another cost ~7 us per call at 512 x 4096 x 4096, r = 16).
+        // first store (loads waited for one after another cost ~4.5 us per call at 512 x 4096 x
+        // 4096, r = 16).
         constexpr int kNV = 4;
-        for (int e0 = tid; e0 < 128 * R; e0 += 512 * kNV) {
+        for (int e0 = tid; e0 < 128 * nr; e0 += 512 * kNV) {
             float tv[kNV], bv[kNV];
 #pragma unroll
             for (int v = 0; v < kNV; ++v) {
                 const int e = e0 + 512 * v;
-                bv[v] = lb[static_cast<size_t>(min(e >> 7, R - 1)) * N + min(nt0 + (e & 127), N - 1)];  // in bounds
+                bv[v] = lb[static_cast<size_t>(r_lo + min(e >> 7, nr - 1)) * N + min(nt0 + (e & 127), N - 1)];  // in bounds
             }
-            lora_t_values<kNV>(tpart, t_splits, M, R, mt0, e0, 512, 128 * R, tv);
+            lora_t_values<kNV>(tpart, t_splits, M, R, r_lo, nr, mt0, e0, 512, 128 * nr, tv);
 #pragma unroll
             for (int v = 0; v < kNV; ++v) {
                 const int e = e0 + 512 * v;
-                if (e < 128 * R) {
-                    const int row = e / R, r = e - row * R;
+                if (e < 128 * nr) {
+                    const int row = e / nr, r = e - row * nr;
                     ts[row * RP + r] = tv[v];
                     bs[e] = bv[v];
                 }
@@ -471,19 +477,19 @@ __global__ __launch_bounds__(512) void q4_gemm_wide_kernel(const uint16_t* xs, c
         const double s = static_cast<double>(lscale) * 0.0625;
         // Eight ranks per pass: every operand of the pass read (unconditionally, at a rank clamped
         // into range) before its MFMAs, which run the two 32-column tiles' chains interleaved; a
-        // rank past R enters as zeros.
+        // rank past nr enters as zeros.
         f32x16 P[2] = {zero16, zero16};
-        for (int r8 = 0; r8 < R; r8 += 8) {
+        for (int r8 = 0; r8 < nr; r8 += 8) {
             float av[4], bv[4][2];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int r = r8 + 2 * j + half, rc = min(r, R - 1);
+                const int r = r8 + 2 * j + half, rc = min(r, nr - 1);
                 const float a = ts[arow * RP + rc];
-                av[j] = r < R ? a : 0.0f;
+                av[j] = r < nr ? a : 0.0f;
 #pragma unroll
                 for (int tn = 0; tn < 2; ++tn) {
                     const float b = bs[rc * 128 + wn * 64 + 32 * tn + col32];
-                    bv[j][tn] = r < R ? b : 0.0f;
+                    bv[j][tn] = r < nr ? b : 0.0f;
                 }
             }
 #pragma unroll
@@ -843,13 +849,39 @@ __global__ __launch_bounds__(256) void prep_kernel(const float* __restrict__ x, 
     lora_t_block(x, la, tpart, M, K, R, b % tiles_m_t, (b / tiles_m_t) % tiles_r, b / (tiles_m_t * tiles_r));
 }
 
-// y[i] = sum_s part[s][i], in ascending s, accumulated in double (K-split
-// partials of the GEMM, and of the LoRA pre-pass T = x * la).
+// y[i] = sum_s part[s][i], in ascending s, accumulated in double (the K-split partials of the
+// GEMM). With vec set (count % 4 == 0 and y 16-byte aligned) a thread takes four consecutive
+// outputs with 16-byte loads and one 16-byte store, all of a pass's loads (up to four partial
+// planes) issued before the first add: at two planes a thread waits for one round of loads per
+// pass instead of one per output.
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ part,
                                                            float* __restrict__ y, size_t count,
-                                                           int splits) {
+                                                           int splits, bool vec) {
     const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
-    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += stride) {
+    const size_t first = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (vec) {  // uniform
+        const size_t quads = count >> 2;
+        for (size_t q = first; q < quads; q += stride) {
+            double s[4] = {0.0, 0.0, 0.0, 0.0};
+            for (int z0 = 0; z0 < splits; z0 += 4) {
+                f32x4 v[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u)  // a plane past the last re-reads the last (in bounds, not added)
+                    v[u] = *reinterpret_cast<const f32x4*>(part + static_cast<size_t>(min(z0 + u, splits - 1)) * count +
+                                                           4 * q);
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (z0 + u < splits)
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) s[c] += static_cast<double>(v[u][c]);
+            }
+            *reinterpret_cast<f32x4*>(y + 4 * q) =
+                f32x4{static_cast<float>(s[0]), static_cast<float>(s[1]), static_cast<float>(s[2]),
+                      static_cast<float>(s[3])};
+        }
+        return;
+    }
+    for (size_t i = first; i < count; i += stride) {
         double s = 0.0;
         int z = 0;
         // eight loads in flight per thread, summed in ascending z
@@ -983,11 +1015,13 @@ hipError_t launch_q4gemm(const Q4Plan& plan, const DeviceInfo& dev, const float*
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess || plan.splits == 1) return e;
     const size_t count = static_cast<size_t>(m) * n;
-    size_t blocks = (count + 255) / 256;
+    // plane z starts z * count floats past the first: 16-byte aligned with the first when count % 4 == 0
+    const bool vec = count % 4 == 0 && ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(partial)) & 15) == 0;
+    size_t blocks = ((vec ? count / 4 : count) + 255) / 256;
     const size_t cap = static_cast<size_t>(dev.cu_count) * 8;
     if (blocks > cap) blocks = cap;
     hipLaunchKernelGGL(split_reduce_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
-                       partial, y, count, plan.splits);
+                       partial, y, count, plan.splits, vec);
     return hipGetLastError();
 }
 

@@ -10,20 +10,20 @@ namespace spaceslug {
 namespace {
 
 // NV values of T for a GEMM epilogue: value v is element e = e0 + stride * v of the row-major
-// block [rows][R] whose first row is row0 (rows past M - 1 clamped to it), the sum of its t_splits
-// partials in double and in split order, rounded once; for e >= count it is a value the caller
-// drops. The loads of kLoraTRound partials of all NV values issue before the first of their sums:
+// block [rows][nr] of T's ranks r_lo .. r_lo + nr - 1 whose first row is row0 (rows past M - 1
+// clamped to it), the sum of its t_splits partials in double and in split order, rounded once;
+// for e >= count it is a value the caller drops. The loads of kLoraTRound partials of all NV values issue before the first of their sums:
 // the epilogue waits for one round of loads per kLoraTRound splits, not for one load after another.
 constexpr int kLoraTRound = 8;
 template <int NV>
-__device__ __forceinline__ void lora_t_values(const float* __restrict__ tpart, int t_splits, int M, int R, int row0,
-                                              int e0, int stride, int count, float (&out)[NV]) {
+__device__ __forceinline__ void lora_t_values(const float* __restrict__ tpart, int t_splits, int M, int R, int r_lo,
+                                              int nr, int row0, int e0, int stride, int count, float (&out)[NV]) {
     size_t idx[NV];
     double t[NV];
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
         const int e = min(e0 + stride * v, count - 1);
-        idx[v] = static_cast<size_t>(min(row0 + e / R, M - 1)) * R + e % R;
+        idx[v] = static_cast<size_t>(min(row0 + e / nr, M - 1)) * R + r_lo + e % nr;
         t[v] = 0.0;
     }
     // Every load unconditional and in bounds (the row clamped, a split past the last one re-reading

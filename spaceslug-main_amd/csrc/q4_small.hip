@@ -409,7 +409,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))) voi
                 const int e = e0 + 64 * W * v;
                 bv[v] = lb[static_cast<size_t>(min(e >> 5, R - 1)) * N + min(n0 + (e & 31), N - 1)];  // in bounds
             }
-            lora_t_values<kNV>(tpart, t_splits, M, R, m0, e0, 64 * W, kDigitRows * R, tv);
+            lora_t_values<kNV>(tpart, t_splits, M, R, 0, R, m0, e0, 64 * W, kDigitRows * R, tv);
 #pragma unroll
             for (int v = 0; v < kNV; ++v) {
                 const int e = e0 + 64 * W * v;
