@@ -96,8 +96,11 @@ __device__ __forceinline__ void split_x_block(const float* __restrict__ x, uint1
         for (int li = 0; li < kLimbs; ++li) limb[li][t] = lo[li] | (hi[li] << 16);
     }
     uint16_t* dst = xs + unit * (kLimbs * kLimbBlockValues) + lane * 8;
+    // Nontemporal: the limbs are read back by the next launch, not by this one (at 512 x 4096 the
+    // preparation launch measured 6.5 -> 5.8 us).
 #pragma unroll
-    for (int li = 0; li < kLimbs; ++li) *reinterpret_cast<u32x4*>(dst + li * kLimbBlockValues) = limb[li];
+    for (int li = 0; li < kLimbs; ++li)
+        __builtin_nontemporal_store(limb[li], reinterpret_cast<u32x4*>(dst + li * kLimbBlockValues));
 }
 
 // Wide tile for M > 32 (prefill, LoRA projections): 128 x 128 outputs per workgroup of 8
