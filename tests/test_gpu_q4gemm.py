@@ -119,10 +119,14 @@ def test_small_m_grid_shapes(session, oracle, gpu, m, n, k):
     check(oracle, got, oracle.q4gemm_packed(c.x, c.packed, c.scales, threads=threads()), label=f"small-m {m}x{n}x{k}")
 
 
+# K-split wide calls sum their partial planes four outputs at a time when M * N % 4 == 0 and one at a
+# time otherwise: (33, 257, 1056) and (45, 99, 4128) take the second form (7 and 26 planes), (44, 100,
+# 4128) the first with a plane count that is not a multiple of four, (40, 100, 14336) with 64 planes.
 @pytest.mark.parametrize("m,n,k", [(40, 100, 32), (200, 130, 64), (129, 1, 96), (40, 100, 14336), (64, 48, 288),
                                    (5, 1, 32), (5, 17, 96), (16, 256, 256), (17, 300, 1024), (32, 64, 64),
                                    (16, 4096, 4064), (9, 40, 128), (31, 33, 384),
-                                   (33, 129, 160), (100, 300, 512), (130, 260, 1056), (256, 512, 2048)])
+                                   (33, 129, 160), (100, 300, 512), (130, 260, 1056), (256, 512, 2048),
+                                   (33, 257, 1056), (45, 99, 4128), (44, 100, 4128)])
 def test_mfma_shapes(session, oracle, gpu, m, n, k):
     note(f"mfma m={m} n={n} k={k}")
     c = make_case(m, n, k)
