@@ -112,20 +112,22 @@ int spaceslug_q4gemm_lora(const float* x, const uint8_t* w_packed, const float* 
                           uint32_t m, uint32_t n, uint32_t k, uint32_t rank, float scale);
 
 /* Device-pointer, stream-ordered variant of spaceslug_q4gemm (no reference
- * counterpart: the reference never passes device memory across its ABI).
- * d_x, d_w_packed must be 16-byte aligned; d_w_scales, d_y 4-byte aligned.
- * Enqueues only. The m <= 4 decode path uses no device memory beyond its
- * arguments; the MFMA path keeps K-split partial sums, and for m > 32 the
- * three bf16 limbs of x (6 * m * k bytes, k rounded up to a multiple of 64), in
- * a library-owned device workspace that is allocated on first use and grown on
- * demand (growth synchronises the device, steady state does
- * not allocate). Calls that share a device share that workspace; the library
+ * counterpart: the reference never passes device memory across its ABI). d_x,
+ * d_w_packed must be 16-byte aligned; d_w_scales, d_y 4-byte aligned.
+ * Enqueues only. Without LoRA, calls of up to 32 rows use no device memory
+ * beyond their arguments; above 32 rows the three bf16 limbs of x (6 * m * k
+ * bytes, m rounded up to a multiple of 16 on the 128 x 128 tiles) and any
+ * K-split partial sums, and in LoRA calls the T = x * lora_a partials, live
+ * in a library-owned device workspace that is allocated on first use and
+ * grown on demand (growth synchronises the device, steady state does not
+ * allocate). Calls that share a device share that workspace; the library
  * orders them: a call on a stream other than the previous user's makes its
  * stream wait (on the GPU, hipStreamWaitEvent) for that user's kernels, and
- * host threads are serialised while enqueueing. A call that needs that workspace
- * returns SPACESLUG_ERR_UNSUPPORTED, enqueueing nothing, while `stream` is being
- * captured into a graph (the graph would keep an address a later, larger call
- * frees): capture a spaceslug_q4_chain or use spaceslug_q4gemm_device_noalloc. */
+ * host threads are serialised while enqueueing. A call that needs that
+ * workspace returns SPACESLUG_ERR_UNSUPPORTED, enqueueing nothing, while
+ * `stream` is being captured into a graph (the graph would keep an address a
+ * later, larger call frees): capture a spaceslug_q4_chain or use
+ * spaceslug_q4gemm_device_noalloc. */
 int spaceslug_q4gemm_device(const float* d_x, const uint8_t* d_w_packed, const float* d_w_scales,
                             float* d_y, uint32_t m, uint32_t n, uint32_t k, void* stream);
 

@@ -45,19 +45,6 @@ __device__ __forceinline__ void nibbles_signed_16th(uint32_t w, float (&f)[8]) {
     f[7] = cvt_off_BYTE_3(wo);
 }
 
-// The same values with compiler-visible instructions only (shifts plus the
-// conversion builtin, about 13 VALU ops). Use this one where the results feed
-// MFMA operands: a VALU result read by an MFMA as SrcB needs two wait states,
-// and after an inline-asm write the compiler inserts only one (s_nop 0 instead
-// of s_nop 1), which gave wrong products on gfx950.
-__device__ __forceinline__ void nibbles_signed_16th_mfma(uint32_t w, float (&f)[8]) {
-#pragma unroll
-    for (int t = 0; t < 8; ++t) f[t] = __builtin_amdgcn_cvt_off_f32_i4(static_cast<int>(w >> (4 * t)));
-}
-
-// Scale that restores nibbles_signed_16th's values to the integers v.
-constexpr float kSixteenthsUnit = 16.0f;
-
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 // x as three bf16 limbs (bit patterns in b[0..2], low 16 bits): b0 is x truncated to its top
@@ -96,29 +83,6 @@ __device__ __forceinline__ u32x4 nibbles_bf16_16th(uint32_t w) {
     for (int t = 0; t < 4; ++t)
         r[t] = __builtin_amdgcn_perm(__float_as_uint(f[2 * t + 1]), __float_as_uint(f[2 * t]), 0x07060302u);
     return r;
-}
-
-// The four 16-lane rows of a wavefront as a 4 x 4 transpose of 32-bit values:
-// on return, register c of row q holds what register q of row c held.
-// v_permlane32_swap exchanges rows 2-3 of its first operand with rows 0-1 of
-// its second, v_permlane16_swap the odd rows of the first with the even rows
-// of the second.
-__device__ __forceinline__ u32x4 transpose_rows(u32x4 r) {
-    const auto p02 = __builtin_amdgcn_permlane32_swap(r.x, r.z, false, false);
-    const auto p13 = __builtin_amdgcn_permlane32_swap(r.y, r.w, false, false);
-    const auto p01 = __builtin_amdgcn_permlane16_swap(p02[0], p13[0], false, false);
-    const auto p23 = __builtin_amdgcn_permlane16_swap(p02[1], p13[1], false, false);
-    return u32x4{p01[0], p01[1], p23[0], p23[1]};
-}
-
-// Row q holds s_q (one value per 16-lane row, per column lane); on return every
-// row holds {s_0, s_1, s_2, s_3}.
-__device__ __forceinline__ f32x4 gather_rows(float s) {
-    const uint32_t u = __float_as_uint(s);
-    const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-    const auto b = __builtin_amdgcn_permlane16_swap(a[0], a[0], false, false);
-    const auto c = __builtin_amdgcn_permlane16_swap(a[1], a[1], false, false);
-    return f32x4{__uint_as_float(b[0]), __uint_as_float(b[1]), __uint_as_float(c[0]), __uint_as_float(c[1])};
 }
 
 // Address of the B operand of lane slot s (column s % 32, word 2 half + s / 32 of the sub-group)
