@@ -1,4 +1,4 @@
-// Decode GEMV for one row: y[n] = sum_k x[k] * v(k, n) * s(n, k/32), K <= 4096.
+// Decode GEMV for one row: y[n] = sum_k x[k] * v(k, n) * s(n, k/32), K <= 32768.
 //
 // HBM-bound: one pass over the packed weights and scales. Work mapping:
 //   - a wavefront owns a run of consecutive columns; lane l owns the scale groups
@@ -12,11 +12,14 @@
 //   - each group sum is formed exactly in integers (v_dot8_i32_i4 on x recoded
 //     as signed hex digits, below) and the group partials are accumulated and
 //     summed over the wavefront in double, so no fp32 rounding touches the sum.
-// Every other shape up to 32 rows (several rows, or K > 4096) is the small-batch
-// GEMM's (q4_small.hip), which forms its group sums the same exact way on the
-// int8 matrix cores.
+// Up to K = 4096 one wavefront takes a whole column (lane l: groups l and l + 64); above, K is
+// split over the wavefronts of a workgroup (q4_gemv_split_kernel). Every other shape up to 32
+// rows (several rows, or K > 32768) is the small-batch GEMM's (q4_small.hip), which forms its
+// group sums the same exact way on the int8 matrix cores.
 #include "q4_device.hpp"
 #include "q4_kernels.hpp"
+
+#include <algorithm>
 
 namespace spaceslug {
 namespace {
@@ -114,6 +117,50 @@ __device__ __forceinline__ void transpose_nibbles(uint32_t (&r)[8]) {
 // Chunk swizzle of the recoded-x staging area (per group: 8 chunks of 16 bytes).
 __device__ __forceinline__ int xds_swizzle(int group) { return (group >> 1) & 7; }
 
+// Recodes half rh (16 values, in xr) of group rg of x into its digit words in xds (layout and
+// swizzle below) and, for rh == 0, writes the group's factor 2^(e_g - 30) to xcs[rg] (0 for
+// rg >= G, NaN when the group holds a non-finite value). The thread holding the other half of
+// the group is the partner lane (lane xor 1).
+__device__ __forceinline__ void recode_x_half(const f32x4 (&xr)[4], int rg, int rh, int G, uint32_t* xds,
+                                              float* xcs) {
+    float m = 0.0f, fin = 1.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            m = fmaxf(m, fabsf(xr[i][c]));  // maxNum: a NaN is caught by fin
+            fin = __builtin_isfinite(xr[i][c]) ? fin : 0.0f;
+        }
+    m = fmaxf(m, dpp_src<0xB1>(m));  // the partner thread holds the group's other half
+    fin = fminf(fin, dpp_src<0xB1>(fin));
+    int e = 0;
+    (void)frexpf(m, &e);  // m < 2^e (e = 0 for m = 0)
+    const bool finite = fin > 0.5f;
+    uint32_t r[2][8];
+#pragma unroll
+    for (int w = 0; w < 2; ++w)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const float v = xr[(8 * w + t) >> 2][t & 3];
+            const int X = finite ? static_cast<int>(rintf(ldexpf(v, kXFracBits - e))) : 0;
+            r[w][t] = (static_cast<uint32_t>(X) + kXBias) ^ 0x88888888u;  // Y, each digit xor 8
+        }
+    // Group rg's 32 digit words as 8 16-byte chunks, chunk c at c ^ xds_swizzle(rg): a
+    // wavefront's 128-bit reads (one group per lane, 128 bytes apart) then hit 16 distinct
+    // 16-byte bank groups per 16 lanes instead of 2 (measured: 84% of the prologue's LDS cycles
+    // were bank conflicts), and the writes 8 instead of 4 per 16 lanes.
+    u32x4* xds4 = reinterpret_cast<u32x4*>(xds);
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+        transpose_nibbles(r[w]);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            xds4[rg * 8 + ((2 * (2 * rh + w) + h) ^ xds_swizzle(rg))] =
+                u32x4{r[w][4 * h], r[w][4 * h + 1], r[w][4 * h + 2], r[w][4 * h + 3]};
+    }
+    if (rh == 0) xcs[rg] = rg >= G ? 0.0f : (finite ? ldexpf(1.0f, e - kXFracBits) : __builtin_nanf(""));
+}
+
 template <int SPC>
 struct PipeSlot {
     u32x4 wv[SPC];
@@ -136,20 +183,28 @@ struct XDigits {
 // (the buffer range check), so it contributes nothing without a per-column select.
 // Weights and scales are read exactly once: nontemporal (aux 2) keeps them from
 // displacing x and each other in the caches.
+// `groups` scale groups of a column from group index `base` (column * G + first group) on; with
+// groups == 0 every load is out of range and reads zeros without touching memory.
 template <int SPC>
-__device__ __forceinline__ void pipe_issue(PipeSlot<SPC>& slot, const u32x4* __restrict__ wq,
-                                           const float* __restrict__ ws, int col, int N, int G,
-                                           const uint32_t (&off16)[SPC], const uint32_t (&off4)[SPC]) {
-    const size_t base = static_cast<size_t>(min(col, N - 1)) * G;
+__device__ __forceinline__ void pipe_issue_groups(PipeSlot<SPC>& slot, const u32x4* __restrict__ wq,
+                                                  const float* __restrict__ ws, size_t base, int groups,
+                                                  const uint32_t (&off16)[SPC], const uint32_t (&off4)[SPC]) {
     const __amdgpu_buffer_rsrc_t rw =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<u32x4*>(wq + base), 0, G * 16, kBufferFlags);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<u32x4*>(wq + base), 0, groups * 16, kBufferFlags);
     const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(ws + base), 0, G * 4, kBufferFlags);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(ws + base), 0, groups * 4, kBufferFlags);
 #pragma unroll
     for (int s = 0; s < SPC; ++s) {
         slot.wv[s] = __builtin_amdgcn_raw_buffer_load_b128(rw, off16[s], 0, kNontemporal);
         slot.sc[s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, off4[s], 0, kNontemporal));
     }
+}
+
+template <int SPC>
+__device__ __forceinline__ void pipe_issue(PipeSlot<SPC>& slot, const u32x4* __restrict__ wq,
+                                           const float* __restrict__ ws, int col, int N, int G,
+                                           const uint32_t (&off16)[SPC], const uint32_t (&off4)[SPC]) {
+    pipe_issue_groups<SPC>(slot, wq, ws, static_cast<size_t>(min(col, N - 1)) * G, G, off16, off4);
 }
 
 // The lane's share of one column (not yet summed over the wavefront).
@@ -253,45 +308,7 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
     }
     asm volatile("" ::: "memory");
 
-    {
-        float m = 0.0f, fin = 1.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                m = fmaxf(m, fabsf(xr[i][c]));  // maxNum: a NaN is caught by fin
-                fin = __builtin_isfinite(xr[i][c]) ? fin : 0.0f;
-            }
-        m = fmaxf(m, dpp_src<0xB1>(m));  // the partner thread holds the group's other half
-        fin = fminf(fin, dpp_src<0xB1>(fin));
-        int e = 0;
-        (void)frexpf(m, &e);  // m < 2^e (e = 0 for m = 0)
-        const bool finite = fin > 0.5f;
-        uint32_t r[2][8];
-#pragma unroll
-        for (int w = 0; w < 2; ++w)
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                const float v = xr[(8 * w + t) >> 2][t & 3];
-                const int X = finite ? static_cast<int>(rintf(ldexpf(v, kXFracBits - e))) : 0;
-                r[w][t] = (static_cast<uint32_t>(X) + kXBias) ^ 0x88888888u;  // Y, each digit xor 8
-            }
-        // Group rg's 32 digit words as 8 16-byte chunks, chunk c at c ^ xds_swizzle(rg): a
-        // wavefront's 128-bit reads (one group per lane, 128 bytes apart) then hit 16 distinct
-        // 16-byte bank groups per 16 lanes instead of 2 (measured: 84% of the prologue's LDS cycles
-        // were bank conflicts), and the writes 8 instead of 4 per 16 lanes.
-        u32x4* xds4 = reinterpret_cast<u32x4*>(xds);
-#pragma unroll
-        for (int w = 0; w < 2; ++w) {
-            transpose_nibbles(r[w]);
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-                xds4[rg * 8 + ((2 * (2 * rh + w) + h) ^ xds_swizzle(rg))] =
-                    u32x4{r[w][4 * h], r[w][4 * h + 1], r[w][4 * h + 2], r[w][4 * h + 3]};
-        }
-        if (rh == 0)
-            xcs[rg] = rg >= G ? 0.0f : (finite ? ldexpf(1.0f, e - kXFracBits) : __builtin_nanf(""));
-    }
+    recode_x_half(xr, rg, rh, G, xds, xcs);
     __syncthreads();
     XDigits<SPC> xd;
 #pragma unroll
@@ -349,6 +366,152 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
     if (lane < cpb && col0 + lane < N) y[col0 + lane] = result;
 }
 
+// Unit i of a column set of the K-split kernel: column col0 + i, groups gb .. gb + gn - 1. A unit
+// past the set (i >= cols) or past N loads nothing.
+template <int SPC>
+__device__ __forceinline__ void pipe_issue_unit(PipeSlot<SPC>& slot, const u32x4* __restrict__ wq,
+                                                const float* __restrict__ ws, int i, int cols, int col0, int N,
+                                                int G, int gb, int gn, const uint32_t (&off16)[SPC],
+                                                const uint32_t (&off4)[SPC]) {
+    const int col = col0 + i;
+    const bool live = i < cols && col < N;
+    pipe_issue_groups<SPC>(slot, wq, ws, static_cast<size_t>(min(col, N - 1)) * G + gb, live ? gn : 0, off16, off4);
+}
+
+// Single-row decode with 32 * kGemvPipeMaxGroups < K <= 32 * kGemvSplitMaxGroups: the kernel
+// above with K split over the wavefronts of a workgroup. KZ wavefronts share a set of `cols`
+// consecutive columns; wavefront z of a set takes groups [z G / KZ, (z + 1) G / KZ) (at most
+// 64 * SPC, lane l holding the part's groups l and l + 64) of every column of the set, so its
+// loads of a column are still one contiguous run; a workgroup of THREADS / 64 wavefronts holds
+// THREADS / (64 KZ) sets. The workgroup recodes all of x into LDS (two threads per group,
+// THREADS / 2 groups per pass), each wavefront keeps the digits of its own groups in registers
+// and streams the set's columns through the same pipeline, and the KZ wave-summed partials of a
+// column are added in double through LDS, in part order (every term exact in double as before;
+// one fp32 rounding of y). The pipeline runs D + S * reps units, at least `cols`: a unit past the
+// set loads nothing and its arithmetic is skipped (a branch on a wavefront-uniform index).
+//
+// The recode of x is the same work in every workgroup (at K = 14336, N = 4096 it ends ~3 us after
+// a wavefront starts, ~1.4 us of it waiting for x), so more wavefronts per SIMD shorten it: at
+// 1 x 4096 x 14336, 64 weight copies, four wavefronts per column took 10.7 us per launch in
+// workgroups of 256 threads, 9.6 in 512 and 9.6-9.7 in 1024 (D = 2); D = 6 at 256 threads 11.4;
+// waiting for x before issuing the first units changed nothing.
+template <int SPC, int D, int KZ, int THREADS>
+__global__ __launch_bounds__(THREADS) void q4_gemv_split_kernel(const float* x,  // not restrict, as above
+                                                               const u32x4* __restrict__ wq,
+                                                               const float* __restrict__ ws,
+                                                               float* __restrict__ y, int N, int K, int cols,
+                                                               int reps) {
+    constexpr int S = D + 1;
+    constexpr int kWaves = THREADS >> 6;
+    constexpr int kSets = kWaves / KZ;                        // column sets per workgroup
+    constexpr int kMaxGroups = 64 * SPC * KZ;                 // G of the largest K (parts of 64 * SPC)
+    constexpr int kPass = THREADS / 2;                        // groups recoded per pass
+    constexpr int kPasses = (kMaxGroups + kPass - 1) / kPass;  // passes for the largest K
+    static_assert(kWaves % KZ == 0 && kMaxGroups % 64 == 0, "whole sets per workgroup");
+    __shared__ __align__(16) uint32_t xds[kPasses * kPass * 4 * kXDigits];
+    __shared__ float xcs[kPasses * kPass];
+    __shared__ double part[kWaves][64];
+    const int lane = threadIdx.x & 63;
+    const int wb = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int z = wb % KZ;
+    const int col0 = (static_cast<int>(blockIdx.x) * kSets + wb / KZ) * cols;
+    const int G = K >> 5;
+    const int gb = z * G / KZ;
+    const int gn = (z + 1) * G / KZ - gb;
+
+    // x first (every pass's loads, groups past G clamped to the last), then the first D units.
+    const int rh = threadIdx.x & 1;
+    f32x4 xr[kPasses][4];
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+        const int rg = min(p * kPass + static_cast<int>(threadIdx.x >> 1), G - 1);
+        const f32x4* src = reinterpret_cast<const f32x4*>(x + static_cast<size_t>(rg) * 32 + rh * 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xr[p][i] = src[i];
+    }
+    asm volatile("" ::: "memory");
+    uint32_t off16[SPC], off4[SPC];
+#pragma unroll
+    for (int s = 0; s < SPC; ++s) {
+        off16[s] = static_cast<uint32_t>(64 * s + lane) * 16u;  // past the part: beyond the buffer, reads 0
+        off4[s] = static_cast<uint32_t>(64 * s + lane) * 4u;
+    }
+    PipeSlot<SPC> slot[S];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        pipe_issue_unit<SPC>(slot[d], wq, ws, d, cols, col0, N, G, gb, gn, off16, off4);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    asm volatile("" ::: "memory");
+
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p)
+        if (p * kPass < G) recode_x_half(xr[p], p * kPass + static_cast<int>(threadIdx.x >> 1), rh, G, xds, xcs);
+    __syncthreads();
+    // Every wavefront scans all G group factors, so the test is the same across the workgroup.
+    float fsum = 0.0f;  // NaN if any factor is (a sum, so that every read issues before the first test)
+#pragma unroll
+    for (int j = 0; j < kMaxGroups / 64; ++j) fsum += xcs[min(64 * j + lane, G - 1)];
+    const bool nonfinite = __builtin_isnan(fsum);
+    if (__builtin_amdgcn_ballot_w64(nonfinite) != 0) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the prologue's column loads
+        if (z == 0) pipe_ieee_columns(x, reinterpret_cast<const uint32_t*>(wq), ws, y, N, G, col0, cols, lane);
+        return;
+    }
+    // The lane's groups gb + l and gb + 64 + l. Entries past the part (the next part's groups, or
+    // past what the passes wrote) meet zero weights (outside the unit's buffer range), and their
+    // factor is taken as 0, so they add nothing.
+    XDigits<SPC> xd;
+#pragma unroll
+    for (int s = 0; s < SPC; ++s) {
+        const int gl = gb + 64 * s + lane;
+        const u32x4* src = reinterpret_cast<const u32x4*>(xds + gl * 4 * kXDigits);
+#pragma unroll
+        for (int q = 0; q < kXDigits; ++q) {
+            const u32x4 t = src[q ^ xds_swizzle(gl)];
+            xd.d[s][4 * q + 0] = t[0];
+            xd.d[s][4 * q + 1] = t[1];
+            xd.d[s][4 * q + 2] = t[2];
+            xd.d[s][4 * q + 3] = t[3];
+        }
+        const float c = xcs[gl];
+        xd.c[s] = 64 * s + lane < gn ? c : 0.0f;
+        xd.cd[s] = static_cast<double>(xd.c[s]);
+    }
+
+    double result = 0.0;
+    for (int r = 0; r < reps; ++r) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const int i = r * S + s;
+            pipe_issue_unit<SPC>(slot[(s + D) % S], wq, ws, i + D, cols, col0, N, G, gb, gn, off16, off4);
+            __builtin_amdgcn_sched_barrier(0);
+            if (i < cols) {
+                const double t = wave_reduce_dpp(pipe_partial<SPC>(slot[s], xd));
+                result = lane == i ? t : result;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+        const int i = reps * S + s;
+        if (i < cols) {
+            const double t = wave_reduce_dpp(pipe_partial<SPC>(slot[s], xd));
+            result = lane == i ? t : result;
+        }
+    }
+    // lane c of each wavefront holds its part of column col0 + c
+    part[wb][lane] = result;
+    __syncthreads();
+    if (z == 0 && lane < cols && col0 + lane < N) {
+        double t = part[wb][lane];
+#pragma unroll
+        for (int q = 1; q < KZ; ++q) t += part[wb + q][lane];
+        y[col0 + lane] = static_cast<float>(t);
+    }
+}
+
 }  // namespace
 
 // Single-row decode with K <= 4096: the pipelined kernel with D = 4 columns in flight
@@ -375,10 +538,36 @@ static hipError_t launch_gemv_pipelined(const DeviceInfo& dev, const float* x, c
     return hipGetLastError();
 }
 
+// Single-row decode with 4096 < K <= 16384: the K-split kernel with KZ = ceil(G / 128) wavefronts
+// per column (parts of 65..128 groups), in workgroups of four column sets (two for KZ = 2, whose
+// smaller sets would leave the pipeline too short at N = 4096): 256, 768 or 1024 threads. Columns
+// per set: the fewest whose workgroups all fit on the CUs at once (at most 64).
+template <int D, int KZ, int THREADS>
+static hipError_t launch_gemv_split(const DeviceInfo& dev, const float* x, const uint8_t* w_packed,
+                                    const float* w_scales, float* y, uint32_t n, uint32_t k, hipStream_t stream) {
+    constexpr int S = D + 1;
+    constexpr size_t kSets = (THREADS / 64) / KZ;
+    const size_t slots = static_cast<size_t>(dev.cu_count) * kSets;  // column sets in one round
+    const size_t cols = std::min<size_t>(64, std::max<size_t>(1, (n + slots - 1) / slots));
+    const int reps = cols > static_cast<size_t>(D) ? static_cast<int>((cols - D + S - 1) / S) : 0;
+    const size_t sets = (n + cols - 1) / cols;
+    const size_t blocks = (sets + kSets - 1) / kSets;
+    hipLaunchKernelGGL((q4_gemv_split_kernel<2, D, KZ, THREADS>), dim3(static_cast<unsigned>(blocks)), dim3(THREADS), 0,
+                       stream, x, reinterpret_cast<const u32x4*>(w_packed), w_scales, y, static_cast<int>(n),
+                       static_cast<int>(k), static_cast<int>(cols), reps);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemv(const DeviceInfo& dev, const float* x, const uint8_t* w_packed, const float* w_scales,
                        float* y, uint32_t m, uint32_t n, uint32_t k, hipStream_t stream) {
-    if (m != 1 || k / kGroup > static_cast<uint32_t>(kGemvPipeMaxGroups)) return hipErrorInvalidValue;
-    return launch_gemv_pipelined(dev, x, w_packed, w_scales, y, n, k, stream);
+    if (m != 1 || k / kGroup > static_cast<uint32_t>(kGemvSplitMaxGroups)) return hipErrorInvalidValue;
+    const uint32_t groups = k / kGroup;
+    if (groups <= static_cast<uint32_t>(kGemvPipeMaxGroups))
+        return launch_gemv_pipelined(dev, x, w_packed, w_scales, y, n, k, stream);
+    if (groups <= 2u * kGemvPipeMaxGroups) return launch_gemv_split<4, 2, 256>(dev, x, w_packed, w_scales, y, n, k, stream);
+    if (groups <= 3u * kGemvPipeMaxGroups) return launch_gemv_split<2, 3, 768>(dev, x, w_packed, w_scales, y, n, k, stream);
+    if (groups <= 4u * kGemvPipeMaxGroups) return launch_gemv_split<2, 4, 1024>(dev, x, w_packed, w_scales, y, n, k, stream);
+    return launch_gemv_split<4, 8, 512>(dev, x, w_packed, w_scales, y, n, k, stream);
 }
 
 }  // namespace spaceslug

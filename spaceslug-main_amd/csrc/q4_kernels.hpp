@@ -16,13 +16,15 @@ constexpr int kGroup = 32;
 // Largest LoRA rank of the fused epilogues (SPACESLUG_Q4_MAX_LORA_RANK in runtime_abi.h).
 constexpr int kMaxLoraRank = 64;
 
-// The decode GEMV takes one row with K <= 32 * kGemvPipeMaxGroups; every other shape up to 32 rows
-// goes to the small-batch GEMM, taller ones to the wide and mid-size kernels.
+// The decode GEMV takes one row with K <= 32 * kGemvSplitMaxGroups (one wavefront per column up to
+// K = 32 * kGemvPipeMaxGroups, K split over a workgroup's wavefronts above); every other shape up to
+// 32 rows goes to the small-batch GEMM, taller ones to the wide and mid-size kernels.
 constexpr int kGemvPipeMaxGroups = 128;
+constexpr int kGemvSplitMaxGroups = 1024;
 
 // Launch shape chosen by plan_q4gemm for one call.
 struct Q4Plan {
-    // kGemv: one-row decode GEMV (k <= 4096, no LoRA); kDigits: every other call up to 32 rows,
+    // kGemv: one-row decode GEMV (k <= 32768, no LoRA); kDigits: every other call up to 32 rows,
     // exact integer group sums on the int8 matrix cores (q4_small.hip); kWide: m > 32; kMid:
     // m > 32 without LoRA whose 128 x 128 grid would need a K-split while its 64 x 64 grid fits
     // the CUs once (k % 64 == 0, k <= 4096).
@@ -40,7 +42,7 @@ struct DeviceInfo {
 // Decides the kernel and K-split for (m, n, k, rank). rank == 0 means no LoRA.
 Q4Plan plan_q4gemm(const DeviceInfo& dev, uint32_t m, uint32_t n, uint32_t k, uint32_t rank);
 
-// Decode GEMV, m == 1 and k <= 32 * kGemvPipeMaxGroups (no device memory beyond its arguments).
+// Decode GEMV, m == 1 and k <= 32 * kGemvSplitMaxGroups (no device memory beyond its arguments).
 hipError_t launch_gemv(const DeviceInfo& dev, const float* x, const uint8_t* w_packed,
                        const float* w_scales, float* y, uint32_t m, uint32_t n, uint32_t k,
                        hipStream_t stream);

@@ -1,4 +1,4 @@
-// Exact small-batch int4 GEMM: M <= 32 rows (and one row with K > 4096), any K % 32 == 0.
+// Exact small-batch int4 GEMM: M <= 32 rows (and one row with K > 32768), any K % 32 == 0.
 //
 // Replaces q4gemm.comp:61-175 for decode-sized batches. Every 32-value group sum
 // sum_k x[m][k] * v[k][n] is formed exactly, in integers, on the int8 matrix cores, in one

@@ -105,6 +105,23 @@ def test_gemv_one_row_column_runs(session, oracle, gpu, n):
     check(oracle, got, oracle.q4gemm_packed(c.x, c.packed, c.scales, threads=threads()), label=f"gemv n={n}")
 
 
+@pytest.mark.parametrize("n,k", [(1, 4128), (7, 4160), (333, 8192), (4097, 8224), (300, 11008), (4096, 14336),
+                                 (5000, 12288), (100, 16384), (1, 16384), (70001, 4160), (40000, 14336),
+                                 (257, 16416), (3000, 20480), (100, 28672), (300, 32768), (1, 32768),
+                                 (257, 32800)])
+def test_gemv_one_row_long_k(session, oracle, gpu, n, k):
+    """One row with K above 4096: K split over ceil(G / 128) wavefronts per column up to K = 16384
+    (two, three or four) and eight above, up to 32768 (parts of 64..128 groups, uneven where G is not
+    a multiple of the split); column sets of 1 to 64 columns (N = 70001 and 40000 use the full 64
+    and more than one round); N = 1 leaves all but one unit of a set empty. K = 32800 is past the
+    kernel and goes to the small-batch GEMM."""
+    m = 1
+    note(f"gemv m={m} n={n} k={k}")
+    c = make_case(m, n, k)
+    got = session.q4gemm_values(c.x, c.packed, c.scales, m, n, k)
+    check(oracle, got, oracle.q4gemm_packed(c.x, c.packed, c.scales, threads=threads()), label=f"gemv {n}x{k}")
+
+
 @pytest.mark.parametrize("m,n,k", [(8, 5000, 512), (9, 4096, 512), (24, 700, 2048), (32, 4096, 1024), (31, 1000, 640),
                                    (2, 9000, 512), (32, 8192, 256), (4, 20000, 256), (17, 14336, 512)])
 def test_small_m_grid_shapes(session, oracle, gpu, m, n, k):
@@ -206,7 +223,7 @@ def magnitude_stress_x(x: np.ndarray, huge: bool) -> np.ndarray:
     return x
 
 
-@pytest.mark.parametrize("k", [4096, 352])
+@pytest.mark.parametrize("k", [4096, 352, 14336])
 def test_one_row_x_groups_of_very_different_magnitude(session, oracle, gpu, k):
     """The one-row kernel recodes x per 32-value group against the group's largest
     magnitude and sums each group exactly in integers: groups of zeros, subnormals,
@@ -235,11 +252,11 @@ def test_multi_row_x_groups_of_very_different_magnitude(session, oracle, gpu, m,
     check(oracle, got, oracle.q4gemm_packed(x, c.packed, c.scales, threads=threads()), label="x magnitudes")
 
 
-@pytest.mark.parametrize("m", [1, 3, 24])
-def test_nan_in_x_gives_nan_outputs(session, oracle, gpu, m):
+@pytest.mark.parametrize("m,k", [(1, 512), (3, 512), (24, 512), (1, 14336)])
+def test_nan_in_x_gives_nan_outputs(session, oracle, gpu, m, k):
     """A NaN in row r of x makes every output of row r NaN, as in the double reference."""
-    note(f"nan in x m={m}")
-    n, k = 64, 512
+    note(f"nan in x m={m} k={k}")
+    n = 64
     c = make_case(m, n, k)
     x = c.x.copy()
     x[0, 77] = np.nan
@@ -250,19 +267,22 @@ def test_nan_in_x_gives_nan_outputs(session, oracle, gpu, m):
         check(oracle, got[1:], oracle.q4gemm_packed(x[1:], c.packed, c.scales), label="rows without nan")
 
 
-@pytest.mark.parametrize("m,k", [(1, 512), (1, 8192), (3, 512), (24, 512), (24, 544), (64, 512), (64, 544)])
+@pytest.mark.parametrize("m,k", [(1, 512), (1, 8192), (1, 14336), (1, 28672), (1, 32800), (3, 512), (24, 512),
+                                 (24, 544), (64, 512), (64, 544)])
 def test_nonfinite_x_matches_reference_pattern(session, oracle, gpu, m, k):
-    """Infinities and NaNs in x on every path: the integer GEMV (1 x 512), the small-batch digit
-    kernel (1 x 8192, 3 and 24 rows), the mid-size bf16-limb kernel (64 x 512) and the wide
-    bf16-limb kernel with a K split and its reduction launch (64 x 544: K % 64 != 0 keeps it off
-    the mid-size kernel). Every output of a row holding a non-finite value is
-    non-finite, NaN exactly where the double reference has NaN (inf * 0, opposite infinities,
-    a NaN) and the same signed infinity elsewhere; rows without one meet the usual bar."""
+    """Infinities and NaNs in x on every path: the integer GEMV (1 x 512), its K-split form
+    (1 x 8192, 1 x 28672, and 1 x 14336 with the infinity in the last group, which only the last
+    of a column's four wavefronts holds), the small-batch digit kernel (1 x 32800, 3 and 24 rows), the
+    mid-size bf16-limb kernel (64 x 512) and the wide bf16-limb kernel with a K split and its
+    reduction launch (64 x 544: K % 64 != 0 keeps it off the mid-size kernel). Every output of a
+    row holding a non-finite value is non-finite, NaN exactly where the double reference has NaN
+    (inf * 0, opposite infinities, a NaN) and the same signed infinity elsewhere; rows without
+    one meet the usual bar."""
     note(f"non-finite x m={m} k={k}")
     n = 300
     c = make_case(m, n, k)
     x = c.x.copy()
-    x[0, 77] = np.inf
+    x[0, 77 if k != 14336 else k - 3] = np.inf
     if m > 1:
         x[1, 5] = np.nan
     if m > 2:

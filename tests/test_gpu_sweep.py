@@ -1,8 +1,9 @@
 """Seeded random shapes through every int4 GEMM path against the oracle, at the stated tolerances.
 
-One decode GEMV row (K up to 4096), the small-batch kernel (2..32 rows, K up to 6400), the wide and
-mid-size MFMA kernels (33..700 rows, K up to 8192, with and without K-splits), and LoRA calls on
-both sides of 32 rows (ranks 1..64), each drawn with the workload distributions (N(0, 1) x, scales
+One decode GEMV row (K up to 4096, and 4128..32768 on its K-split form), the small-batch kernel
+(2..32 rows, K up to 6400), the wide and mid-size MFMA kernels (33..700 rows, K up to 8192, with
+and without K-splits), and LoRA calls on both sides of 32 rows (ranks 1..64), each drawn with the
+workload distributions (N(0, 1) x, scales
 in [0.01, 0.05]) or the reference KAT's ranges (x in [-1, 1), scales in [0.5, 1.5);
 test_q4gemm.cpp:168-176). Bars: 1e-5 up to 32 rows (exact group sums), 6e-6 * sqrt(K / 32)
 (at least 1e-5) above, as the header states them.
@@ -70,3 +71,23 @@ def test_random_shapes_match_oracle(session, oracle, gpu, case):
     assert got.shape == (m, n) and np.all(np.isfinite(got))
     rep = oracle.compare(got, want, bar)
     assert rep["status"] == "pass", (case, rep["max_relative_error"], bar)
+
+
+def long_k_cases(seed: int, count: int):
+    rng = random.Random(seed)
+    return [(rng.randint(1, 5000), 32 * rng.randint(129, 1024), rng.choice(("normal", "uniform")), rng.getrandbits(32),
+             rng.getrandbits(32), rng.getrandbits(32)) for _ in range(count)]
+
+
+@pytest.mark.parametrize("case", long_k_cases(0x10C4, 16), ids=lambda c: f"gemv-1x{c[0]}x{c[1]}-{c[2]}")
+def test_random_long_k_rows_match_oracle(session, oracle, gpu, case):
+    """One row with K from 4128 to 32768 (the K-split decode GEMV), at the 1e-5 bar."""
+    n, k, dist, sa, sb, ss = case
+    note(f"sweep gemv-long m=1 n={n} k={k} {dist}")
+    scale_range = (0.01, 0.05) if dist == "normal" else (0.5, 1.5)
+    c = make_case(1, n, k, x_dist=dist, scale_range=scale_range, seed_a=sa, seed_b=sb, seed_s=ss)
+    got = session.q4gemm_values(c.x, c.packed, c.scales, 1, n, k)
+    want = oracle.q4gemm_packed(c.x, c.packed, c.scales, threads=min(16, os.cpu_count() or 1))
+    assert got.shape == (1, n) and np.all(np.isfinite(got))
+    rep = oracle.compare(got, want, 1e-5)
+    assert rep["status"] == "pass", (case, rep["max_relative_error"])
