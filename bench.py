@@ -27,6 +27,9 @@ least 15 HIP-event-timed iterations after warm-up:
     4 * 2*M'*N*K int8 ops with M' = M rounded up to 8 rows, below int8's machine balance, so that leg's
     roofline is HBM (algorithmic bytes against 8 TB/s) with the int8 MFMA rate against 5.0 POP/s beside it;
   - "small_batch" (M=16, K=N=4096, 32 weight copies per step) and "lora" (M=512, K=N=4096, rank 16);
+  - "decode_down": one row through the transposed shape, K=14336, N=4096 (the MLP's down projection;
+    64 weight copies per step, the same 36.7 MB per call as the headline), which takes the K-split
+    form of the decode GEMV;
   - "reference_bench": the reference's own q4gemm benchmark configuration (bench_q4gemm.cpp: M=N=K=1024,
     its LCG generators and seeds, 128 warm-ups, median of 15 timed calls, TFLOP/s = 2*N^3 / time);
   - "cq4": the CQ4 codebook matmul on the reference's CQ4 benchmark shapes;
@@ -62,7 +65,9 @@ HBM_PEAK_GBS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 INT8_MFMA_PEAK_TOPS = 5000.0
-# Up to 32 rows the library runs v_mfma_i32_32x32x32_i8 on x as 4 byte digits, 8 rows per tile.
+# One row with K up to this is the decode GEMV (VALU integer dot products); other calls up to 32 rows run
+# v_mfma_i32_32x32x32_i8 on x as 4 byte digits, 8 rows per tile.
+GEMV_MAX_K = 32768
 DIGITS = 4
 DIGIT_ROWS = 8
 # The library runs GEMMs of more than 32 rows on the bf16 MFMA with x as three exact bf16 limbs.
@@ -75,7 +80,8 @@ def gemm_roofline(m: int, n: int, k: int, seconds_per_call: float) -> dict:
     """Roofline of the GEMM kernel that runs m x n x k. Above 32 rows: the matrix instruction's executed flops
     per second against that instruction's dense peak (LoRA's rank-r terms, under 1% of the work, are left out).
     Up to 32 rows the int8 digit MFMA executes fewer ops per byte than int8's machine balance (625 per byte
-    of HBM), so the bound is HBM; the int8 rate is reported beside it."""
+    of HBM), so the bound is HBM; the int8 rate is reported beside it. One row with K <= 32768 is the decode
+    GEMV (v_dot8_i32_i4 on VALU, no matrix instruction): HBM alone."""
     tf = 2.0 * m * n * k / seconds_per_call / 1e12
     if m >= WIDE_MIN_ROWS:
         achieved = BF16_LIMBS * tf
@@ -84,6 +90,10 @@ def gemm_roofline(m: int, n: int, k: int, seconds_per_call: float) -> dict:
                 "frac": round(achieved / BF16_MFMA_PEAK_TFLOPS, 4), "fp32_equivalent_tflops": round(tf, 2),
                 "fp32_mfma_peak": FP32_MFMA_PEAK_TFLOPS}
     gbs = algo_bytes(m, n, k) / seconds_per_call / 1e9
+    if m == 1 and k <= GEMV_MAX_K:
+        return {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4), "kernel": "decode GEMV (v_dot8_i32_i4), K split over a workgroup"
+                if k > 4096 else "decode GEMV (v_dot8_i32_i4)"}
     rows = (m + DIGIT_ROWS - 1) // DIGIT_ROWS * DIGIT_ROWS
     tops = DIGITS * 2.0 * rows * n * k / seconds_per_call / 1e12
     return {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -798,6 +808,12 @@ def main() -> int:
         checks["small_batch"] = sb.pop("check")
         result["small_batch"] = gemm_entry(sb, unit_gbs=True)
         torch.cuda.empty_cache()
+        print("[bench] decode down projection 1x14336->4096 x64 copies", file=sys.stderr, flush=True)
+        dd = bench_gemm(torch, session, 1, 4096, 14336, copies=64, iters=iters, warmup=3)
+        checks["decode_down"] = dd.pop("check")
+        result["decode_down"] = gemm_entry(dd, unit_gbs=True)
+        result["decode_down"]["hbm_frac"] = round(dd["gbs"] / 8000.0, 4)
+        torch.cuda.empty_cache()
         print("[bench] lora 512x4096x4096 r16", file=sys.stderr, flush=True)
         lo = bench_gemm(torch, session, 512, 4096, 4096, copies=1, iters=iters, warmup=3, rank=16)
         checks["lora"] = lo.pop("check")
@@ -827,7 +843,8 @@ def main() -> int:
         # stated tolerance for those is 6e-6 * sqrt(K / 32) (one fp32 rounding per MFMA of each group's ~30x
         # larger partial sum; 3.4e-5 at K = 1024); the workload configurations are held to 1e-5.
         plan = (("prefill", max(args.cpu_seconds, 30.0), 8, 1e-5), ("small_batch", 3.0, 16, 1e-5),
-                ("lora", 6.0, 8, 1e-5), ("reference_bench", 3.0, 64, bf16_limb_tolerance(1024)))
+                ("decode_down", 3.0, 1, 1e-5), ("lora", 6.0, 8, 1e-5),
+                ("reference_bench", 3.0, 64, bf16_limb_tolerance(1024)))
         for name, budget, single, bar in plan:
             if name in checks:
                 print(f"[bench] cpu baseline + parity: {name}", file=sys.stderr, flush=True)
