@@ -914,9 +914,7 @@ size_t split_x_bf16_bytes(uint32_t m, uint32_t k) {
 
 Q4Plan plan_q4gemm(const DeviceInfo& dev, uint32_t m, uint32_t n, uint32_t k, uint32_t rank) {
     Q4Plan plan{Q4Plan::kGemv, 1, 0, 0};
-    if (rank == 0 && m == 1 && k / kGroup <= static_cast<uint32_t>(kGemvSplitMaxGroups)) {
-        return plan;
-    }
+    if (rank == 0 && gemv_takes(m, k)) return plan;
     const int groups = static_cast<int>(k / kGroup);
     size_t lora_bytes = 0;
     if (rank > 0) {

@@ -1,4 +1,5 @@
-// Decode GEMV for one row: y[n] = sum_k x[k] * v(k, n) * s(n, k/32), K <= 32768.
+// Decode GEMV: y[m][n] = sum_k x[m][k] * v(k, n) * s(n, k/32) for one row (K <= 32768) or two
+// rows (2048 <= K <= 4096).
 //
 // HBM-bound: one pass over the packed weights and scales. Work mapping:
 //   - a wavefront owns a run of consecutive columns; lane l owns the scale groups
@@ -12,10 +13,10 @@
 //   - each group sum is formed exactly in integers (v_dot8_i32_i4 on x recoded
 //     as signed hex digits, below) and the group partials are accumulated and
 //     summed over the wavefront in double, so no fp32 rounding touches the sum.
-// Up to K = 4096 one wavefront takes a whole column (lane l: groups l and l + 64); above, K is
-// split over the wavefronts of a workgroup (q4_gemv_split_kernel). Every other shape up to 32
-// rows (several rows, or K > 32768) is the small-batch GEMM's (q4_small.hip), which forms its
-// group sums the same exact way on the int8 matrix cores.
+// Up to K = 4096 one wavefront takes a whole column (lane l: groups l and l + 64) for one or two
+// rows, each weight load serving both; above, K is split over the wavefronts of a workgroup
+// (q4_gemv_split_kernel, one row). Every other shape up to 32 rows is the small-batch GEMM's
+// (q4_small.hip), which forms its group sums the same exact way on the int8 matrix cores.
 #include "q4_device.hpp"
 #include "q4_kernels.hpp"
 
@@ -52,7 +53,7 @@ __device__ __forceinline__ double wave_reduce_dpp(double v) {
     return __hiloint2double(hi, lo);
 }
 
-// Software-pipelined single-row decode (M = 1, K <= 4096) in integer arithmetic.
+// Software-pipelined decode of MR rows (MR = 1 or 2, K <= 4096) in integer arithmetic.
 //
 // x is recoded once per workgroup. For each 32-value group g, with e_g the
 // exponent for which max|x| < 2^e_g, X_k = rint(x_k * 2^(30 - e_g)) is an integer
@@ -264,16 +265,17 @@ __device__ __forceinline__ void pipe_ieee_columns(const float* x, const uint32_t
     }
 }
 
-template <int SPC, int D>
+template <int SPC, int D, int MR>
 __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float* x,  // not restrict: x loads stay ahead of the weights
                                                                    const u32x4* __restrict__ wq,
                                                                    const float* __restrict__ ws,
                                                                    float* __restrict__ y, int N, int K, int reps) {
-    constexpr int S = D + 1;           // register slots
-    constexpr int kGroups = 64 * SPC;  // groups per lane pass: K <= 32 * kGroups
-    static_assert(kGroups * 2 == kGemvThreads, "x is recoded by two threads per group");
-    __shared__ __align__(16) uint32_t xds[kGroups * 4 * kXDigits];
-    __shared__ float xcs[kGroups];
+    constexpr int S = D + 1;                      // register slots
+    constexpr int kGroups = 64 * SPC;             // groups per lane pass: K <= 32 * kGroups
+    constexpr int kRecoded = kGemvThreads / 2;    // groups recoded (two threads per group)
+    static_assert(kGroups <= kRecoded, "x is recoded by two threads per group");
+    __shared__ __align__(16) uint32_t xds[MR][kRecoded * 4 * kXDigits];
+    __shared__ float xcs[MR][kRecoded];
     const int lane = threadIdx.x & 63;
     const int wave =
         __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x * (kGemvThreads >> 6) + (threadIdx.x >> 6)));
@@ -283,14 +285,16 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
     const int col0 = wave * cpb;
     const int G = K >> 5;
 
-    // x first (thread t recodes half t & 1, 16 values, of group t >> 1), then the
+    // x first (thread t recodes half t & 1, 16 values, of group t >> 1 of every row), then the
     // first D columns, all before any wait.
     const int rg = threadIdx.x >> 1, rh = threadIdx.x & 1;
-    f32x4 xr[4];
-    {
-        const f32x4* src = reinterpret_cast<const f32x4*>(x + static_cast<size_t>(min(rg, G - 1)) * 32 + rh * 16);
+    f32x4 xr[MR][4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) xr[i] = src[i];
+    for (int r = 0; r < MR; ++r) {
+        const f32x4* src =
+            reinterpret_cast<const f32x4*>(x + static_cast<size_t>(r) * K + static_cast<size_t>(min(rg, G - 1)) * 32 + rh * 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xr[r][i] = src[i];
     }
     asm volatile("" ::: "memory");
     uint32_t off16[SPC], off4[SPC];
@@ -308,50 +312,62 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
     }
     asm volatile("" ::: "memory");
 
-    recode_x_half(xr, rg, rh, G, xds, xcs);
+#pragma unroll
+    for (int r = 0; r < MR; ++r) recode_x_half(xr[r], rg, rh, G, xds[r], xcs[r]);
     __syncthreads();
-    XDigits<SPC> xd;
+    XDigits<SPC> xd[MR];
 #pragma unroll
-    for (int s = 0; s < SPC; ++s) {
-        const int gl = 64 * s + lane;
-        const u32x4* src = reinterpret_cast<const u32x4*>(xds + gl * 4 * kXDigits);
+    for (int r = 0; r < MR; ++r)
 #pragma unroll
-        for (int q = 0; q < kXDigits; ++q) {
-            const u32x4 t = src[q ^ xds_swizzle(gl)];
-            xd.d[s][4 * q + 0] = t[0];
-            xd.d[s][4 * q + 1] = t[1];
-            xd.d[s][4 * q + 2] = t[2];
-            xd.d[s][4 * q + 3] = t[3];
+        for (int s = 0; s < SPC; ++s) {
+            const int gl = 64 * s + lane;
+            const u32x4* src = reinterpret_cast<const u32x4*>(xds[r] + gl * 4 * kXDigits);
+#pragma unroll
+            for (int q = 0; q < kXDigits; ++q) {
+                const u32x4 t = src[q ^ xds_swizzle(gl)];
+                xd[r].d[s][4 * q + 0] = t[0];
+                xd[r].d[s][4 * q + 1] = t[1];
+                xd[r].d[s][4 * q + 2] = t[2];
+                xd[r].d[s][4 * q + 3] = t[3];
+            }
+            xd[r].c[s] = xcs[r][gl];
+            xd[r].cd[s] = static_cast<double>(xd[r].c[s]);
         }
-        xd.c[s] = xcs[gl];
-        xd.cd[s] = static_cast<double>(xd.c[s]);
-    }
     // The wavefront's lanes cover every group of x, so this test is the same in every
     // wavefront of the grid (uniform): with a non-finite x the integer form has nothing to
-    // carry it, and the columns are taken by the IEEE path below instead.
+    // carry it, and the columns of every row are taken by the IEEE path below instead.
     bool nonfinite = false;
 #pragma unroll
-    for (int s = 0; s < SPC; ++s) nonfinite = nonfinite || __builtin_isnan(xd.c[s]);
+    for (int r = 0; r < MR; ++r)
+#pragma unroll
+        for (int s = 0; s < SPC; ++s) nonfinite = nonfinite || __builtin_isnan(xd[r].c[s]);
     if (__builtin_amdgcn_ballot_w64(nonfinite) != 0) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the prologue's column loads
-        pipe_ieee_columns(x, reinterpret_cast<const uint32_t*>(wq), ws, y, N, G, col0, cpb, lane);
+        for (int r = 0; r < MR; ++r)
+            pipe_ieee_columns(x + static_cast<size_t>(r) * K, reinterpret_cast<const uint32_t*>(wq), ws,
+                              y + static_cast<size_t>(r) * N, N, G, col0, cpb, lane);
         return;
     }
 
     // Steady state, S columns per trip: issue column i + D into the free slot, then compute
-    // column i (slot i % S). The sched barriers keep each column's arithmetic between its
-    // own issue points: interleaved slots would make the wavefront wait for every
+    // column i (slot i % S) for every row. The sched barriers keep each column's arithmetic
+    // between its own issue points: interleaved slots would make the wavefront wait for every
     // outstanding load first. (Reducing four columns at once with fewer instructions
     // measured slower: the wavefront then waits out one long dependent chain per four.)
-    float result = 0.0f;
-    for (int r = 0; r < reps; ++r) {
+    float result[MR];
+#pragma unroll
+    for (int r = 0; r < MR; ++r) result[r] = 0.0f;
+    for (int rep = 0; rep < reps; ++rep) {
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-            const int i = r * S + s;
+            const int i = rep * S + s;
             pipe_issue<SPC>(slot[(s + D) % S], wq, ws, col0 + i + D, N, G, off16, off4);
             __builtin_amdgcn_sched_barrier(0);
-            const float t = static_cast<float>(wave_reduce_dpp(pipe_partial<SPC>(slot[s], xd)));
-            result = lane == i ? t : result;
+#pragma unroll
+            for (int r = 0; r < MR; ++r) {
+                const float t = static_cast<float>(wave_reduce_dpp(pipe_partial<SPC>(slot[s], xd[r])));
+                result[r] = lane == i ? t : result[r];
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
     }
@@ -359,11 +375,16 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_pipe_kernel(const float*
 #pragma unroll
     for (int s = 0; s < D; ++s) {
         const int i = reps * S + s;
-        const float t = static_cast<float>(wave_reduce_dpp(pipe_partial<SPC>(slot[s], xd)));
-        result = lane == i ? t : result;
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+            const float t = static_cast<float>(wave_reduce_dpp(pipe_partial<SPC>(slot[s], xd[r])));
+            result[r] = lane == i ? t : result[r];
+        }
     }
-    // lane c holds column col0 + c: one coalesced store of the wavefront's run
-    if (lane < cpb && col0 + lane < N) y[col0 + lane] = result;
+    // lane c holds column col0 + c: one coalesced store of the wavefront's run per row
+    if (lane < cpb && col0 + lane < N)
+#pragma unroll
+        for (int r = 0; r < MR; ++r) y[static_cast<size_t>(r) * N + col0 + lane] = result[r];
 }
 
 // Unit i of a column set of the K-split kernel: column col0 + i, groups gb .. gb + gn - 1. A unit
@@ -514,14 +535,18 @@ __global__ __launch_bounds__(THREADS) void q4_gemv_split_kernel(const float* x, 
 
 }  // namespace
 
-// Single-row decode with K <= 4096: the pipelined kernel with D = 4 columns in flight
-// per wavefront. Columns per wavefront: the fewest (cpb = 4 + 5 * reps, at most 64)
+// Decode of one or two rows with K <= 4096: the pipelined kernel with D = 4 columns in flight
+// per wavefront (one lane slot per group up to K = 2048, two above). Columns per wavefront: the fewest (cpb = 4 + 5 * reps, at most 64)
 // whose workgroups of 4 wavefronts all fit on the CUs at once, so no workgroup waits
 // for a second round. At K = 4096, N = 14336 that is 14 columns, 1024 wavefronts:
 // 7.48 us per launch, against 7.9-8.1 us for D = 2..5 at 15-19 columns, 8.3 us for
 // D = 1 and 9-10 us for all columns in flight at once; a grid 8% over one round
 // (276 workgroups) took 11.9 us. 7 columns at D = 3 (two wavefronts per SIMD)
-// measured the same within 1%.
+// measured the same within 1%. Two rows share every weight load and double the arithmetic:
+// 2 x 4096 -> 14336 takes 11.5 us against 14.8 for the small-batch GEMM (2 x 2048 -> 4096: 4.5
+// against 5.7 us). One lane slot at K <= 2048 keeps half the lanes from computing on zeros:
+// 1 x 2048 -> 14336 5.4 us against 6.8.
+template <int MR>
 static hipError_t launch_gemv_pipelined(const DeviceInfo& dev, const float* x, const uint8_t* w_packed,
                                  const float* w_scales, float* y, uint32_t n, uint32_t k, hipStream_t stream) {
     constexpr int D = 4, S = D + 1, kMaxReps = (64 - D) / S;
@@ -532,16 +557,22 @@ static hipError_t launch_gemv_pipelined(const DeviceInfo& dev, const float* x, c
     const size_t cpb = D + S * reps;
     const size_t waves = (static_cast<size_t>(n) + cpb - 1) / cpb;
     const size_t blocks = (waves + waves_per_block - 1) / waves_per_block;
-    hipLaunchKernelGGL((q4_gemv_pipe_kernel<2, D>), dim3(static_cast<unsigned>(blocks)), dim3(kGemvThreads), 0,
-                       stream, x, reinterpret_cast<const u32x4*>(w_packed), w_scales, y, static_cast<int>(n),
-                       static_cast<int>(k), reps);
+    if (k / kGroup <= 64u)  // one group per lane: no idle second slot
+        hipLaunchKernelGGL((q4_gemv_pipe_kernel<1, D, MR>), dim3(static_cast<unsigned>(blocks)), dim3(kGemvThreads), 0,
+                           stream, x, reinterpret_cast<const u32x4*>(w_packed), w_scales, y, static_cast<int>(n),
+                           static_cast<int>(k), reps);
+    else
+        hipLaunchKernelGGL((q4_gemv_pipe_kernel<2, D, MR>), dim3(static_cast<unsigned>(blocks)), dim3(kGemvThreads), 0,
+                           stream, x, reinterpret_cast<const u32x4*>(w_packed), w_scales, y, static_cast<int>(n),
+                           static_cast<int>(k), reps);
     return hipGetLastError();
 }
 
-// Single-row decode with 4096 < K <= 16384: the K-split kernel with KZ = ceil(G / 128) wavefronts
-// per column (parts of 65..128 groups), in workgroups of four column sets (two for KZ = 2, whose
-// smaller sets would leave the pipeline too short at N = 4096): 256, 768 or 1024 threads. Columns
-// per set: the fewest whose workgroups all fit on the CUs at once (at most 64).
+// Single-row decode with 4096 < K <= 32768: the K-split kernel with KZ = ceil(G / 128) wavefronts
+// per column up to K = 16384 and eight above (parts of 64..128 groups), in workgroups of four
+// column sets (two for KZ = 2, whose smaller sets would leave the pipeline too short at N = 4096;
+// one for KZ = 8): 256, 768, 1024 or 512 threads. Columns per set: the fewest whose workgroups all
+// fit on the CUs at once (at most 64).
 template <int D, int KZ, int THREADS>
 static hipError_t launch_gemv_split(const DeviceInfo& dev, const float* x, const uint8_t* w_packed,
                                     const float* w_scales, float* y, uint32_t n, uint32_t k, hipStream_t stream) {
@@ -560,10 +591,11 @@ static hipError_t launch_gemv_split(const DeviceInfo& dev, const float* x, const
 
 hipError_t launch_gemv(const DeviceInfo& dev, const float* x, const uint8_t* w_packed, const float* w_scales,
                        float* y, uint32_t m, uint32_t n, uint32_t k, hipStream_t stream) {
-    if (m != 1 || k / kGroup > static_cast<uint32_t>(kGemvSplitMaxGroups)) return hipErrorInvalidValue;
+    if (!gemv_takes(m, k)) return hipErrorInvalidValue;
+    if (m == 2) return launch_gemv_pipelined<2>(dev, x, w_packed, w_scales, y, n, k, stream);
     const uint32_t groups = k / kGroup;
     if (groups <= static_cast<uint32_t>(kGemvPipeMaxGroups))
-        return launch_gemv_pipelined(dev, x, w_packed, w_scales, y, n, k, stream);
+        return launch_gemv_pipelined<1>(dev, x, w_packed, w_scales, y, n, k, stream);
     if (groups <= 2u * kGemvPipeMaxGroups) return launch_gemv_split<4, 2, 256>(dev, x, w_packed, w_scales, y, n, k, stream);
     if (groups <= 3u * kGemvPipeMaxGroups) return launch_gemv_split<2, 3, 768>(dev, x, w_packed, w_scales, y, n, k, stream);
     if (groups <= 4u * kGemvPipeMaxGroups) return launch_gemv_split<2, 4, 1024>(dev, x, w_packed, w_scales, y, n, k, stream);

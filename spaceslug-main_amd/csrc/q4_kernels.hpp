@@ -22,9 +22,17 @@ constexpr int kMaxLoraRank = 64;
 constexpr int kGemvPipeMaxGroups = 128;
 constexpr int kGemvSplitMaxGroups = 1024;
 
+// Shapes the decode GEMV takes: one row with K <= 32 * kGemvSplitMaxGroups, or two rows with
+// 2048 <= K <= 32 * kGemvPipeMaxGroups (one weight load serves both rows; below K = 2048 half of
+// each wavefront's lanes would idle and the small-batch GEMM is as fast).
+constexpr bool gemv_takes(uint32_t m, uint32_t k) {
+    return (m == 1 && k / kGroup <= static_cast<uint32_t>(kGemvSplitMaxGroups)) ||
+           (m == 2 && k >= 2048 && k / kGroup <= static_cast<uint32_t>(kGemvPipeMaxGroups));
+}
+
 // Launch shape chosen by plan_q4gemm for one call.
 struct Q4Plan {
-    // kGemv: one-row decode GEMV (k <= 32768, no LoRA); kDigits: every other call up to 32 rows,
+    // kGemv: decode GEMV (gemv_takes, no LoRA); kDigits: every other call up to 32 rows,
     // exact integer group sums on the int8 matrix cores (q4_small.hip); kWide: m > 32; kMid:
     // m > 32 without LoRA whose 128 x 128 grid would need a K-split while its 64 x 64 grid fits
     // the CUs once (k % 64 == 0, k <= 4096).
@@ -42,7 +50,7 @@ struct DeviceInfo {
 // Decides the kernel and K-split for (m, n, k, rank). rank == 0 means no LoRA.
 Q4Plan plan_q4gemm(const DeviceInfo& dev, uint32_t m, uint32_t n, uint32_t k, uint32_t rank);
 
-// Decode GEMV, m == 1 and k <= 32 * kGemvSplitMaxGroups (no device memory beyond its arguments).
+// Decode GEMV for the shapes gemv_takes accepts (no device memory beyond its arguments).
 hipError_t launch_gemv(const DeviceInfo& dev, const float* x, const uint8_t* w_packed,
                        const float* w_scales, float* y, uint32_t m, uint32_t n, uint32_t k,
                        hipStream_t stream);

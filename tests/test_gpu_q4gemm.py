@@ -122,6 +122,20 @@ def test_gemv_one_row_long_k(session, oracle, gpu, n, k):
     check(oracle, got, oracle.q4gemm_packed(c.x, c.packed, c.scales, threads=threads()), label=f"gemv {n}x{k}")
 
 
+@pytest.mark.parametrize("n,k", [(1, 2048), (7, 2080), (4097, 2048), (9001, 4096), (333, 4064), (14337, 3008),
+                                 (200003, 2048), (50, 2016)])
+def test_gemv_two_rows(session, oracle, gpu, n, k):
+    """Two rows on the decode GEMV (2048 <= K <= 4096): one weight load per column serves both rows;
+    one lane slot per group at K = 2048, two above (the second partly empty at 2080, 3008, 4064);
+    N from 1 to 200003 (the maximum run of 64 columns per wavefront). K = 2016 stays on the
+    small-batch GEMM."""
+    m = 2
+    note(f"gemv m={m} n={n} k={k}")
+    c = make_case(m, n, k)
+    got = session.q4gemm_values(c.x, c.packed, c.scales, m, n, k)
+    check(oracle, got, oracle.q4gemm_packed(c.x, c.packed, c.scales, threads=threads()), label=f"gemv 2x{n}x{k}")
+
+
 @pytest.mark.parametrize("m,n,k", [(8, 5000, 512), (9, 4096, 512), (24, 700, 2048), (32, 4096, 1024), (31, 1000, 640),
                                    (2, 9000, 512), (32, 8192, 256), (4, 20000, 256), (17, 14336, 512)])
 def test_small_m_grid_shapes(session, oracle, gpu, m, n, k):
@@ -252,7 +266,7 @@ def test_multi_row_x_groups_of_very_different_magnitude(session, oracle, gpu, m,
     check(oracle, got, oracle.q4gemm_packed(x, c.packed, c.scales, threads=threads()), label="x magnitudes")
 
 
-@pytest.mark.parametrize("m,k", [(1, 512), (3, 512), (24, 512), (1, 14336)])
+@pytest.mark.parametrize("m,k", [(1, 512), (3, 512), (24, 512), (1, 14336), (2, 2048)])
 def test_nan_in_x_gives_nan_outputs(session, oracle, gpu, m, k):
     """A NaN in row r of x makes every output of row r NaN, as in the double reference."""
     note(f"nan in x m={m} k={k}")
@@ -267,14 +281,16 @@ def test_nan_in_x_gives_nan_outputs(session, oracle, gpu, m, k):
         check(oracle, got[1:], oracle.q4gemm_packed(x[1:], c.packed, c.scales), label="rows without nan")
 
 
-@pytest.mark.parametrize("m,k", [(1, 512), (1, 8192), (1, 14336), (1, 28672), (1, 32800), (3, 512), (24, 512),
-                                 (24, 544), (64, 512), (64, 544)])
+@pytest.mark.parametrize("m,k", [(1, 512), (1, 8192), (1, 14336), (1, 28672), (1, 32800), (2, 4096), (3, 512),
+                                 (24, 512), (24, 544), (64, 512), (64, 544)])
 def test_nonfinite_x_matches_reference_pattern(session, oracle, gpu, m, k):
     """Infinities and NaNs in x on every path: the integer GEMV (1 x 512), its K-split form
     (1 x 8192, 1 x 28672, and 1 x 14336 with the infinity in the last group, which only the last
-    of a column's four wavefronts holds), the small-batch digit kernel (1 x 32800, 3 and 24 rows), the
-    mid-size bf16-limb kernel (64 x 512) and the wide bf16-limb kernel with a K split and its
-    reduction launch (64 x 544: K % 64 != 0 keeps it off the mid-size kernel). Every output of a
+    of a column's four wavefronts holds), its two-row form (2 x 4096, the second row finite: it is
+    then formed by the same IEEE path and meets the usual bar), the small-batch digit kernel
+    (1 x 32800, 3 and 24 rows), the mid-size bf16-limb kernel (64 x 512) and the wide bf16-limb
+    kernel with a K split and its reduction launch (64 x 544: K % 64 != 0 keeps it off the
+    mid-size kernel). Every output of a
     row holding a non-finite value is non-finite, NaN exactly where the double reference has NaN
     (inf * 0, opposite infinities, a NaN) and the same signed infinity elsewhere; rows without
     one meet the usual bar."""
@@ -283,9 +299,8 @@ def test_nonfinite_x_matches_reference_pattern(session, oracle, gpu, m, k):
     c = make_case(m, n, k)
     x = c.x.copy()
     x[0, 77 if k != 14336 else k - 3] = np.inf
-    if m > 1:
-        x[1, 5] = np.nan
     if m > 2:
+        x[1, 5] = np.nan
         x[2, 40] = -np.inf
         x[2, 300] = np.inf
     if m > 3:
