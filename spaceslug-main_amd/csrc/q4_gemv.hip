@@ -399,11 +399,11 @@ __device__ __forceinline__ void pipe_issue_unit(PipeSlot<SPC>& slot, const u32x4
     pipe_issue_groups<SPC>(slot, wq, ws, static_cast<size_t>(min(col, N - 1)) * G + gb, live ? gn : 0, off16, off4);
 }
 
-// Single-row decode with 32 * kGemvPipeMaxGroups < K <= 32 * kGemvSplitMaxGroups: the kernel
-// above with K split over the wavefronts of a workgroup. KZ wavefronts share a set of `cols`
-// consecutive columns; wavefront z of a set takes groups [z G / KZ, (z + 1) G / KZ) (at most
-// 64 * SPC, lane l holding the part's groups l and l + 64) of every column of the set, so its
-// loads of a column are still one contiguous run; a workgroup of THREADS / 64 wavefronts holds
+// Decode of MR rows (one or two) with K > 32 * kGemvPipeMaxGroups: the kernel above with K split
+// over the wavefronts of a workgroup. KZ wavefronts share a set of `cols` consecutive columns;
+// wavefront z of a set takes groups [z G / KZ, (z + 1) G / KZ) (at most 64 * SPC, lane l holding
+// the part's groups l, l + 64, ...) of every column of the set, so its loads of a column are
+// still one contiguous run, each serving every row; a workgroup of THREADS / 64 wavefronts holds
 // THREADS / (64 KZ) sets. The workgroup recodes all of x into LDS (two threads per group,
 // THREADS / 2 groups per pass), each wavefront keeps the digits of its own groups in registers
 // and streams the set's columns through the same pipeline, and the KZ wave-summed partials of a
@@ -413,10 +413,10 @@ __device__ __forceinline__ void pipe_issue_unit(PipeSlot<SPC>& slot, const u32x4
 //
 // The recode of x is the same work in every workgroup (at K = 14336, N = 4096 it ends ~3 us after
 // a wavefront starts, ~1.4 us of it waiting for x), so more wavefronts per SIMD shorten it: at
-// 1 x 4096 x 14336, 64 weight copies, four wavefronts per column took 10.7 us per launch in
+// one row, K = 14336, N = 4096, 64 weight copies, four wavefronts per column took 10.7 us per launch in
 // workgroups of 256 threads, 9.6 in 512 and 9.6-9.7 in 1024 (D = 2); D = 6 at 256 threads 11.4;
 // waiting for x before issuing the first units changed nothing.
-template <int SPC, int D, int KZ, int THREADS>
+template <int SPC, int D, int KZ, int THREADS, int MR>
 __global__ __launch_bounds__(THREADS) void q4_gemv_split_kernel(const float* x,  // not restrict, as above
                                                                const u32x4* __restrict__ wq,
                                                                const float* __restrict__ ws,
@@ -429,9 +429,9 @@ __global__ __launch_bounds__(THREADS) void q4_gemv_split_kernel(const float* x, 
     constexpr int kPass = THREADS / 2;                        // groups recoded per pass
     constexpr int kPasses = (kMaxGroups + kPass - 1) / kPass;  // passes for the largest K
     static_assert(kWaves % KZ == 0 && kMaxGroups % 64 == 0, "whole sets per workgroup");
-    __shared__ __align__(16) uint32_t xds[kPasses * kPass * 4 * kXDigits];
-    __shared__ float xcs[kPasses * kPass];
-    __shared__ double part[kWaves][64];
+    __shared__ __align__(16) uint32_t xds[MR][kPasses * kPass * 4 * kXDigits];
+    __shared__ float xcs[MR][kPasses * kPass];
+    __shared__ double part[kWaves][MR][64];
     const int lane = threadIdx.x & 63;
     const int wb = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int z = wb % KZ;
@@ -440,16 +440,20 @@ __global__ __launch_bounds__(THREADS) void q4_gemv_split_kernel(const float* x, 
     const int gb = z * G / KZ;
     const int gn = (z + 1) * G / KZ - gb;
 
-    // x first (every pass's loads, groups past G clamped to the last), then the first D units.
+    // x first (every row's and pass's loads, groups past G clamped to the last), then the first D
+    // units.
     const int rh = threadIdx.x & 1;
-    f32x4 xr[kPasses][4];
+    f32x4 xr[MR][kPasses][4];
 #pragma unroll
-    for (int p = 0; p < kPasses; ++p) {
-        const int rg = min(p * kPass + static_cast<int>(threadIdx.x >> 1), G - 1);
-        const f32x4* src = reinterpret_cast<const f32x4*>(x + static_cast<size_t>(rg) * 32 + rh * 16);
+    for (int r = 0; r < MR; ++r)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) xr[p][i] = src[i];
-    }
+        for (int p = 0; p < kPasses; ++p) {
+            const int rg = min(p * kPass + static_cast<int>(threadIdx.x >> 1), G - 1);
+            const f32x4* src =
+                reinterpret_cast<const f32x4*>(x + static_cast<size_t>(r) * K + static_cast<size_t>(rg) * 32 + rh * 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xr[r][p][i] = src[i];
+        }
     asm volatile("" ::: "memory");
     uint32_t off16[SPC], off4[SPC];
 #pragma unroll
@@ -466,50 +470,66 @@ __global__ __launch_bounds__(THREADS) void q4_gemv_split_kernel(const float* x, 
     asm volatile("" ::: "memory");
 
 #pragma unroll
-    for (int p = 0; p < kPasses; ++p)
-        if (p * kPass < G) recode_x_half(xr[p], p * kPass + static_cast<int>(threadIdx.x >> 1), rh, G, xds, xcs);
+    for (int r = 0; r < MR; ++r)
+#pragma unroll
+        for (int p = 0; p < kPasses; ++p)
+            if (p * kPass < G)
+                recode_x_half(xr[r][p], p * kPass + static_cast<int>(threadIdx.x >> 1), rh, G, xds[r], xcs[r]);
     __syncthreads();
-    // Every wavefront scans all G group factors, so the test is the same across the workgroup.
+    // Every wavefront scans all G group factors of every row, so the test is the same across the
+    // workgroup.
     float fsum = 0.0f;  // NaN if any factor is (a sum, so that every read issues before the first test)
 #pragma unroll
-    for (int j = 0; j < kMaxGroups / 64; ++j) fsum += xcs[min(64 * j + lane, G - 1)];
+    for (int r = 0; r < MR; ++r)
+#pragma unroll
+        for (int j = 0; j < kMaxGroups / 64; ++j) fsum += xcs[r][min(64 * j + lane, G - 1)];
     const bool nonfinite = __builtin_isnan(fsum);
     if (__builtin_amdgcn_ballot_w64(nonfinite) != 0) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the prologue's column loads
-        if (z == 0) pipe_ieee_columns(x, reinterpret_cast<const uint32_t*>(wq), ws, y, N, G, col0, cols, lane);
+        if (z == 0)
+            for (int r = 0; r < MR; ++r)
+                pipe_ieee_columns(x + static_cast<size_t>(r) * K, reinterpret_cast<const uint32_t*>(wq), ws,
+                                  y + static_cast<size_t>(r) * N, N, G, col0, cols, lane);
         return;
     }
     // The lane's groups gb + l and gb + 64 + l. Entries past the part (the next part's groups, or
     // past what the passes wrote) meet zero weights (outside the unit's buffer range), and their
     // factor is taken as 0, so they add nothing.
-    XDigits<SPC> xd;
+    XDigits<SPC> xd[MR];
 #pragma unroll
-    for (int s = 0; s < SPC; ++s) {
-        const int gl = gb + 64 * s + lane;
-        const u32x4* src = reinterpret_cast<const u32x4*>(xds + gl * 4 * kXDigits);
+    for (int r = 0; r < MR; ++r)
 #pragma unroll
-        for (int q = 0; q < kXDigits; ++q) {
-            const u32x4 t = src[q ^ xds_swizzle(gl)];
-            xd.d[s][4 * q + 0] = t[0];
-            xd.d[s][4 * q + 1] = t[1];
-            xd.d[s][4 * q + 2] = t[2];
-            xd.d[s][4 * q + 3] = t[3];
+        for (int s = 0; s < SPC; ++s) {
+            const int gl = gb + 64 * s + lane;
+            const u32x4* src = reinterpret_cast<const u32x4*>(xds[r] + gl * 4 * kXDigits);
+#pragma unroll
+            for (int q = 0; q < kXDigits; ++q) {
+                const u32x4 t = src[q ^ xds_swizzle(gl)];
+                xd[r].d[s][4 * q + 0] = t[0];
+                xd[r].d[s][4 * q + 1] = t[1];
+                xd[r].d[s][4 * q + 2] = t[2];
+                xd[r].d[s][4 * q + 3] = t[3];
+            }
+            const float c = xcs[r][gl];
+            xd[r].c[s] = 64 * s + lane < gn ? c : 0.0f;
+            xd[r].cd[s] = static_cast<double>(xd[r].c[s]);
         }
-        const float c = xcs[gl];
-        xd.c[s] = 64 * s + lane < gn ? c : 0.0f;
-        xd.cd[s] = static_cast<double>(xd.c[s]);
-    }
 
-    double result = 0.0;
-    for (int r = 0; r < reps; ++r) {
+    double result[MR];
+#pragma unroll
+    for (int r = 0; r < MR; ++r) result[r] = 0.0;
+    for (int rep = 0; rep < reps; ++rep) {
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-            const int i = r * S + s;
+            const int i = rep * S + s;
             pipe_issue_unit<SPC>(slot[(s + D) % S], wq, ws, i + D, cols, col0, N, G, gb, gn, off16, off4);
             __builtin_amdgcn_sched_barrier(0);
             if (i < cols) {
-                const double t = wave_reduce_dpp(pipe_partial<SPC>(slot[s], xd));
-                result = lane == i ? t : result;
+#pragma unroll
+                for (int r = 0; r < MR; ++r) {
+                    const double t = wave_reduce_dpp(pipe_partial<SPC>(slot[s], xd[r]));
+                    result[r] = lane == i ? t : result[r];
+                }
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -518,19 +538,25 @@ __global__ __launch_bounds__(THREADS) void q4_gemv_split_kernel(const float* x, 
     for (int s = 0; s < D; ++s) {
         const int i = reps * S + s;
         if (i < cols) {
-            const double t = wave_reduce_dpp(pipe_partial<SPC>(slot[s], xd));
-            result = lane == i ? t : result;
+#pragma unroll
+            for (int r = 0; r < MR; ++r) {
+                const double t = wave_reduce_dpp(pipe_partial<SPC>(slot[s], xd[r]));
+                result[r] = lane == i ? t : result[r];
+            }
         }
     }
-    // lane c of each wavefront holds its part of column col0 + c
-    part[wb][lane] = result;
-    __syncthreads();
-    if (z == 0 && lane < cols && col0 + lane < N) {
-        double t = part[wb][lane];
+    // lane c of each wavefront holds its part of column col0 + c of every row
 #pragma unroll
-        for (int q = 1; q < KZ; ++q) t += part[wb + q][lane];
-        y[col0 + lane] = static_cast<float>(t);
-    }
+    for (int r = 0; r < MR; ++r) part[wb][r][lane] = result[r];
+    __syncthreads();
+    if (z == 0 && lane < cols && col0 + lane < N)
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+            double t = part[wb][r][lane];
+#pragma unroll
+            for (int q = 1; q < KZ; ++q) t += part[wb + q][r][lane];
+            y[static_cast<size_t>(r) * N + col0 + lane] = static_cast<float>(t);
+        }
 }
 
 }  // namespace
@@ -573,7 +599,7 @@ static hipError_t launch_gemv_pipelined(const DeviceInfo& dev, const float* x, c
 // column sets (two for KZ = 2, whose smaller sets would leave the pipeline too short at N = 4096;
 // one for KZ = 8): 256, 768, 1024 or 512 threads. Columns per set: the fewest whose workgroups all
 // fit on the CUs at once (at most 64).
-template <int D, int KZ, int THREADS>
+template <int D, int KZ, int THREADS, int MR = 1, int SPC = 2>
 static hipError_t launch_gemv_split(const DeviceInfo& dev, const float* x, const uint8_t* w_packed,
                                     const float* w_scales, float* y, uint32_t n, uint32_t k, hipStream_t stream) {
     constexpr int S = D + 1;
@@ -583,7 +609,7 @@ static hipError_t launch_gemv_split(const DeviceInfo& dev, const float* x, const
     const int reps = cols > static_cast<size_t>(D) ? static_cast<int>((cols - D + S - 1) / S) : 0;
     const size_t sets = (n + cols - 1) / cols;
     const size_t blocks = (sets + kSets - 1) / kSets;
-    hipLaunchKernelGGL((q4_gemv_split_kernel<2, D, KZ, THREADS>), dim3(static_cast<unsigned>(blocks)), dim3(THREADS), 0,
+    hipLaunchKernelGGL((q4_gemv_split_kernel<SPC, D, KZ, THREADS, MR>), dim3(static_cast<unsigned>(blocks)), dim3(THREADS), 0,
                        stream, x, reinterpret_cast<const u32x4*>(w_packed), w_scales, y, static_cast<int>(n),
                        static_cast<int>(k), static_cast<int>(cols), reps);
     return hipGetLastError();
@@ -592,8 +618,21 @@ static hipError_t launch_gemv_split(const DeviceInfo& dev, const float* x, const
 hipError_t launch_gemv(const DeviceInfo& dev, const float* x, const uint8_t* w_packed, const float* w_scales,
                        float* y, uint32_t m, uint32_t n, uint32_t k, hipStream_t stream) {
     if (!gemv_takes(m, k)) return hipErrorInvalidValue;
-    if (m == 2) return launch_gemv_pipelined<2>(dev, x, w_packed, w_scales, y, n, k, stream);
     const uint32_t groups = k / kGroup;
+    if (m == 2) {
+        if (groups <= static_cast<uint32_t>(kGemvPipeMaxGroups))
+            return launch_gemv_pipelined<2>(dev, x, w_packed, w_scales, y, n, k, stream);
+        // Two rows' digits of two groups per lane take 128 registers, so the K-split forms run at
+        // most two wavefronts per SIMD; between K = 8192 and 12288, where four parts of two lane
+        // slots would leave a third of the lanes idle, six parts of one slot (3 per SIMD) instead:
+        // 2 x 11008 -> 8192 20.8 against 23.8 us (one slot at K = 8192 or 14336 is slower: 11.3
+        // against 10.0 and 17.1 against 15.4 us).
+        if (groups <= 2u * kGemvPipeMaxGroups)
+            return launch_gemv_split<4, 2, 256, 2>(dev, x, w_packed, w_scales, y, n, k, stream);
+        if (groups <= 3u * kGemvPipeMaxGroups)
+            return launch_gemv_split<3, 6, 768, 2, 1>(dev, x, w_packed, w_scales, y, n, k, stream);
+        return launch_gemv_split<3, 4, 512, 2>(dev, x, w_packed, w_scales, y, n, k, stream);
+    }
     if (groups <= static_cast<uint32_t>(kGemvPipeMaxGroups))
         return launch_gemv_pipelined<1>(dev, x, w_packed, w_scales, y, n, k, stream);
     if (groups <= 2u * kGemvPipeMaxGroups) return launch_gemv_split<4, 2, 256>(dev, x, w_packed, w_scales, y, n, k, stream);

@@ -23,11 +23,12 @@ constexpr int kGemvPipeMaxGroups = 128;
 constexpr int kGemvSplitMaxGroups = 1024;
 
 // Shapes the decode GEMV takes: one row with K <= 32 * kGemvSplitMaxGroups, or two rows with
-// 2048 <= K <= 32 * kGemvPipeMaxGroups (one weight load serves both rows; below K = 2048 half of
-// each wavefront's lanes would idle and the small-batch GEMM is as fast).
+// 2048 <= K <= 16384 (one weight load serves both rows; below K = 2048 half of each wavefront's
+// lanes would idle and the small-batch GEMM is as fast; above 16384 two rows' recoded x would not
+// fit the LDS).
 constexpr bool gemv_takes(uint32_t m, uint32_t k) {
     return (m == 1 && k / kGroup <= static_cast<uint32_t>(kGemvSplitMaxGroups)) ||
-           (m == 2 && k >= 2048 && k / kGroup <= static_cast<uint32_t>(kGemvPipeMaxGroups));
+           (m == 2 && k >= 2048 && k / kGroup <= 4u * static_cast<uint32_t>(kGemvPipeMaxGroups));
 }
 
 // Launch shape chosen by plan_q4gemm for one call.

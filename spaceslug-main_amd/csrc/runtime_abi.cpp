@@ -419,7 +419,7 @@ int spaceslug_sgemm(const float* a, const float* b, float* c, uint32_t m, uint32
 
 const char* spaceslug_q4gemm_capability(void) {
     return "q4gemm-hip-gfx950 group=32 layout=n-major-lsb-nibble "
-           "decode=gemv(m=1,k<=32768 or m=2,2048<=k<=4096: x as hex digits, v_dot8_i32_i4, exact group sums, k>4096 split over a workgroup) "
+           "decode=gemv(m=1,k<=32768 or m=2,2048<=k<=16384: x as hex digits, v_dot8_i32_i4, exact group sums, k>4096 split over a workgroup) "
            "small=mfma(m<=32: x as byte digits, v_mfma_i32_32x32x32_i8, exact group sums) "
            "gemm=mfma(m>32: v_mfma_f32_32x32x16_bf16 on 3 exact x limbs, 128x128 tiles with K-split or 64x64 "
            "whole-K tiles; f32 group sums) accumulate=f64-over-groups lora=fused-epilogue(rank<=64) "

@@ -123,12 +123,14 @@ def test_gemv_one_row_long_k(session, oracle, gpu, n, k):
 
 
 @pytest.mark.parametrize("n,k", [(1, 2048), (7, 2080), (4097, 2048), (9001, 4096), (333, 4064), (14337, 3008),
-                                 (200003, 2048), (50, 2016)])
+                                 (200003, 2048), (50, 2016), (1, 4128), (4096, 8192), (300, 11008), (4096, 14336),
+                                 (40000, 12288), (77, 16384), (257, 16416)])
 def test_gemv_two_rows(session, oracle, gpu, n, k):
-    """Two rows on the decode GEMV (2048 <= K <= 4096): one weight load per column serves both rows;
-    one lane slot per group at K = 2048, two above (the second partly empty at 2080, 3008, 4064);
-    N from 1 to 200003 (the maximum run of 64 columns per wavefront). K = 2016 stays on the
-    small-batch GEMM."""
+    """Two rows on the decode GEMV (2048 <= K <= 16384): one weight load per column serves both
+    rows; one lane slot per group at K = 2048, two above (the second partly empty at 2080, 3008,
+    4064); N from 1 to 200003 (the maximum run of 64 columns per wavefront); above K = 4096 the
+    K-split form with two or four wavefronts per column (N = 40000 fills 64-column sets). K = 2016
+    and K = 16416 stay on the small-batch GEMM."""
     m = 2
     note(f"gemv m={m} n={n} k={k}")
     c = make_case(m, n, k)
@@ -281,13 +283,14 @@ def test_nan_in_x_gives_nan_outputs(session, oracle, gpu, m, k):
         check(oracle, got[1:], oracle.q4gemm_packed(x[1:], c.packed, c.scales), label="rows without nan")
 
 
-@pytest.mark.parametrize("m,k", [(1, 512), (1, 8192), (1, 14336), (1, 28672), (1, 32800), (2, 4096), (3, 512),
-                                 (24, 512), (24, 544), (64, 512), (64, 544)])
+@pytest.mark.parametrize("m,k", [(1, 512), (1, 8192), (1, 14336), (1, 28672), (1, 32800), (2, 4096), (2, 14336),
+                                 (3, 512), (24, 512), (24, 544), (64, 512), (64, 544)])
 def test_nonfinite_x_matches_reference_pattern(session, oracle, gpu, m, k):
     """Infinities and NaNs in x on every path: the integer GEMV (1 x 512), its K-split form
     (1 x 8192, 1 x 28672, and 1 x 14336 with the infinity in the last group, which only the last
-    of a column's four wavefronts holds), its two-row form (2 x 4096, the second row finite: it is
-    then formed by the same IEEE path and meets the usual bar), the small-batch digit kernel
+    of a column's four wavefronts holds), its two-row forms (2 x 4096 and 2 x 14336, with the
+    infinity in the last group; the second row finite: it is then formed by the same IEEE path and
+    meets the usual bar), the small-batch digit kernel
     (1 x 32800, 3 and 24 rows), the mid-size bf16-limb kernel (64 x 512) and the wide bf16-limb
     kernel with a K split and its reduction launch (64 x 544: K % 64 != 0 keeps it off the
     mid-size kernel). Every output of a
