@@ -555,17 +555,21 @@ def test_split_k_calls_on_two_streams(session, oracle, gpu, m, n, k):
         check(oracle, ys[i].cpu().numpy(), want[i], label=f"stream {i}")
 
 
-@pytest.mark.parametrize("m,entry", [(1, "device"), (16, "device"), (16, "noalloc")])
-def test_projection_chain_in_a_hip_graph(session, oracle, gpu, m, entry):
+@pytest.mark.parametrize("m,entry,k1,n1,n2", [(1, "device", 512, 1024, 384), (16, "device", 512, 1024, 384),
+                                              (16, "noalloc", 512, 1024, 384), (1, "device", 14336, 4096, 8192),
+                                              (1, "noalloc", 28672, 1024, 512), (2, "device", 8192, 4096, 2048),
+                                              (2, "noalloc", 12288, 2048, 1024)])
+def test_projection_chain_in_a_hip_graph(session, oracle, gpu, m, entry, k1, n1, n2):
     """Two chained projections (y1 = x W1, y2 = y1 W2) captured once in a HIP graph and replayed with new
     inputs: every replay equals the eager chain bit for bit. Calls of up to 32 rows without LoRA need no
     library workspace (one launch each), so the device entry point captures them; so does the entry
-    point that allocates nothing."""
+    point that allocates nothing. Covered: the small-batch GEMM (16 rows), the one-row GEMV at K = 512
+    and 4096, its K-split form (K = 14336 and 28672, then 4096 and 1024), and the two-row forms (K = 8192
+    then 4096, K = 12288 then 2048)."""
     import torch
 
-    note(f"graph chain m={m} entry={entry}")
+    note(f"graph chain m={m} entry={entry} k1={k1} n1={n1} n2={n2}")
     call = session.q4gemm_device if entry == "device" else session.q4gemm_device_noalloc
-    k1, n1, n2 = 512, 1024, 384
     c1 = make_case(m, n1, k1, seed_b=0x51, seed_s=0x52)
     c2 = make_case(m, n2, n1, seed_b=0x61, seed_s=0x62)
     w1, s1 = to_dev(c1.packed, torch), to_dev(c1.scales, torch)

@@ -13,9 +13,10 @@ from cases import lora_factors, make_case
 
 pytestmark = pytest.mark.gpu
 
-# (m, n, k, rank): GEMV, small batch, K-split wide, mid-size tiles, LoRA on both sides of 32 rows
-SHAPES = [(1, 3000, 4096, 0), (7, 900, 1024, 0), (40, 300, 4128, 0), (100, 301, 512, 0), (64, 256, 1024, 8),
-          (5, 700, 2048, 4)]
+# (m, n, k, rank): GEMV (one row; K-split; two rows), small batch, K-split wide, mid-size tiles, LoRA on both
+# sides of 32 rows
+SHAPES = [(1, 3000, 4096, 0), (1, 2000, 14336, 0), (2, 900, 8192, 0), (7, 900, 1024, 0), (40, 300, 4128, 0),
+          (100, 301, 512, 0), (64, 256, 1024, 8), (5, 700, 2048, 4)]
 THREADS = 8
 ROUNDS = 4
 
