@@ -5,8 +5,8 @@ The reference's KAT and bench draw x uniform in [-1, 1) and scales uniform in [0
 group's partial sum is ~15, ~30x the workload configurations' (scales 0.01-0.05), while outputs near
 zero are held to an absolute 1e-5 by the metric |gpu - ref| / max(1, |ref|) (test_q4gemm.cpp:380).
 
-Up to 32 rows every path forms each group sum exactly in integers (the one-row decode GEMV with
-v_dot8 on hex digits of x, the small-batch GEMM with int8 MFMAs on byte digits of x) and sums the
+Up to 32 rows every path forms each group sum exactly in integers (the one- and two-row decode GEMV
+with v_dot8 on hex digits of x, the small-batch GEMM with int8 MFMAs on byte digits of x) and sums the
 groups in double. The only approximation left is x's 31-bit fixed point per group (at most 2^-30 of
 the group's largest |x| per value), so these cases are held to 2e-7: a few fp32 roundings of y
 itself. An fp32 group sum measured 2e-5 to 8e-5 on the same inputs, so a return of one fails here.
@@ -51,8 +51,10 @@ def run_and_check(session, oracle, c, tol: float, label: str) -> float:
 
 @pytest.mark.parametrize("m,k", [(1, 1024), (1, 4096), (1, 8192), (2, 1024), (2, 4096), (4, 1024), (4, 4096),
                                  (3, 8192), (16, 1024), (16, 4096), (32, 1024), (32, 4096), (32, 8192),
-                                 (24, 640), (7, 2080)])
+                                 (24, 640), (7, 2080), (1, 14336), (1, 32768), (2, 8192), (2, 11008), (2, 16384)])
 def test_small_batch_exact_on_kat_ranges(session, oracle, gpu, m, k):
+    """Every path up to 32 rows, including the decode GEMV's K-split forms (one row up to K = 32768, two
+    rows up to 16384), whose per-wavefront partials are added in double."""
     n = 2048 if k <= 4096 else 1024
     note(f"kat ranges m={m} n={n} k={k}")
     c = make_case(m, n, k, **KAT_RANGES)
