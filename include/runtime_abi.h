@@ -43,7 +43,8 @@
  *     (2^-24 |y|) plus the fixed-point rounding of x, at most 2^-30 of the
  *     group's largest |x| per value: <= 2e-7 on the reference KAT's input ranges
  *     (x in [-1, 1), scales in [0.5, 1.5); test_q4gemm.cpp:168-176), asserted for
- *     m = 1..32 at K up to 8192 (the decode GEMV up to K = 32768), and on x whose groups span 1e-30..1e30.
+ *     m = 1..32 at K up to 8192 (the decode GEMV up to K = 32768), and on x
+ *     whose groups span 1e-30..1e30.
  *   - m > 32 (bf16 MFMA on x split exactly into three bf16 limbs; every product
  *     exact, one fp32 rounding per MFMA of each 32-value group sum, groups summed
  *     in double): the error grows like sqrt(K / 32). Stated tolerance
