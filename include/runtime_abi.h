@@ -95,7 +95,7 @@ const char* spaceslug_q4gemm_capability(void);
 const char* spaceslug_last_error(void);
 
 /* Replaces q4gemm.comp:61-175 as dispatched by test_q4gemm.cpp:335-356, as a
- * C-ABI call: synchronous host pointers, any m >= 1 and n >= 1, k % 32 == 0
+ * C-ABI call: synchronous host pointers, any 1 <= m, n <= 2^31 - 2^16, k % 32 == 0
  * (the reference shader additionally needs m % 64 == 0 and n % 64 == 0,
  * q4gemm.comp:36-37). */
 int spaceslug_q4gemm(const float* x, const uint8_t* w_packed, const float* w_scales, float* y,

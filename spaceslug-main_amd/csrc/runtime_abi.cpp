@@ -195,9 +195,13 @@ private:
     std::vector<size_t> offsets_;
 };
 
+// Row and column counts stay below 2^31 - 2^16, so that a kernel's int indices past the last row
+// or column (a partly filled workgroup or column run reaches at most 2^16 beyond) cannot wrap.
+constexpr uint32_t kMaxRowsCols = INT32_MAX - 65535u;
+
 bool dims_ok(uint32_t m, uint32_t n, uint32_t k) {
-    return m >= 1 && n >= 1 && k >= 32 && (k % spaceslug::kGroup) == 0 && m <= INT32_MAX &&
-           n <= INT32_MAX && k <= INT32_MAX;
+    return m >= 1 && n >= 1 && k >= 32 && (k % spaceslug::kGroup) == 0 && m <= kMaxRowsCols &&
+           n <= kMaxRowsCols && k <= INT32_MAX;
 }
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
@@ -360,7 +364,7 @@ const char* device_call_problem(const float* d_x, const uint8_t* d_w_packed, con
                                 const float* d_lora_a, const float* d_lora_b, float* d_y, uint32_t m, uint32_t n,
                                 uint32_t k, uint32_t rank) {
     if (!d_x || !d_w_packed || !d_w_scales || !d_y) return "null pointer";
-    if (!dims_ok(m, n, k)) return "need m>=1, n>=1, k%32==0";
+    if (!dims_ok(m, n, k)) return "need 1<=m,n<=2^31-2^16, k%32==0";
     if (!aligned(d_x, 16) || !aligned(d_w_packed, 16) || !aligned(d_w_scales, 4) || !aligned(d_y, 4))
         return "misaligned device pointer";
     if (d_lora_a || d_lora_b) {
@@ -431,7 +435,7 @@ const char* spaceslug_last_error(void) { return g_last_error.c_str(); }
 int spaceslug_q4gemm(const float* x, const uint8_t* w_packed, const float* w_scales, float* y, uint32_t m,
                      uint32_t n, uint32_t k) {
     if (!x || !w_packed || !w_scales || !y) return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm: null pointer");
-    if (!dims_ok(m, n, k)) return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm: need m>=1, n>=1, k>=32, k%32==0");
+    if (!dims_ok(m, n, k)) return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm: need 1<=m,n<=2^31-2^16, k>=32, k%32==0");
     try {
         return run_host(x, w_packed, w_scales, nullptr, nullptr, nullptr, nullptr, y, m, n, k, 0, 0.0f);
     } catch (const HipError& e) {
@@ -449,7 +453,7 @@ int spaceslug_q4gemm_lora(const float* x, const uint8_t* w_packed, const float* 
     if (!x || !w_packed || !w_scales || !lora_a || !lora_b || !y)
         return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_lora: null pointer");
     if (!dims_ok(m, n, k) || rank == 0 || rank > SPACESLUG_Q4_MAX_LORA_RANK)
-        return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_lora: need m>=1, n>=1, k%32==0, 1<=rank<=64");
+        return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_lora: need 1<=m,n<=2^31-2^16, k%32==0, 1<=rank<=64");
     try {
         return run_host(x, w_packed, w_scales, nullptr, nullptr, lora_a, lora_b, y, m, n, k, rank, scale);
     } catch (const HipError& e) {
@@ -465,7 +469,7 @@ int spaceslug_q4gemm_device(const float* d_x, const uint8_t* d_w_packed, const f
                             uint32_t m, uint32_t n, uint32_t k, void* stream) {
     if (!d_x || !d_w_packed || !d_w_scales || !d_y)
         return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_device: null pointer");
-    if (!dims_ok(m, n, k)) return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_device: need m>=1, n>=1, k%32==0");
+    if (!dims_ok(m, n, k)) return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_device: need 1<=m,n<=2^31-2^16, k%32==0");
     if (!aligned(d_x, 16) || !aligned(d_w_packed, 16) || !aligned(d_w_scales, 4) || !aligned(d_y, 4))
         return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_device: misaligned device pointer");
     try {
@@ -512,7 +516,7 @@ int spaceslug_q4gemm_lora_device(const float* d_x, const uint8_t* d_w_packed, co
     if (!d_x || !d_w_packed || !d_w_scales || !d_lora_a || !d_lora_b || !d_y)
         return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_lora_device: null pointer");
     if (!dims_ok(m, n, k) || rank == 0 || rank > SPACESLUG_Q4_MAX_LORA_RANK)
-        return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_lora_device: need m>=1, n>=1, k%32==0, 1<=rank<=64");
+        return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_lora_device: need 1<=m,n<=2^31-2^16, k%32==0, 1<=rank<=64");
     if (!aligned(d_x, 16) || !aligned(d_w_packed, 16) || !aligned(d_w_scales, 4) || !aligned(d_y, 4) ||
         !aligned(d_lora_a, 4) || !aligned(d_lora_b, 4))
         return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_lora_device: misaligned device pointer");
@@ -615,7 +619,7 @@ int spaceslug_q4_quantize_device(const float* d_w, uint8_t* d_w_packed, float* d
 
 int spaceslug_q4gemm_run(const spaceslug_q4_weight* weight, const float* x, float* y, uint32_t m) {
     if (!weight || !x || !y) return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_run: null pointer");
-    if (!dims_ok(m, weight->n, weight->k)) return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_run: need m>=1");
+    if (!dims_ok(m, weight->n, weight->k)) return fail(SPACESLUG_ERR_INVALID, "spaceslug_q4gemm_run: need 1<=m<=2^31-2^16");
     try {
         int cur = -1;
         check(hipGetDevice(&cur), "hipGetDevice");

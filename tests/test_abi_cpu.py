@@ -96,7 +96,8 @@ def test_q4gemm_rejects_invalid_arguments(lib):
     assert call(_p(x), None, _p(s), _p(y), 2, 8, 64) == 1
     assert call(_p(x), _p(w, u8p), None, _p(y), 2, 8, 64) == 1
     assert call(_p(x), _p(w, u8p), _p(s), None, 2, 8, 64) == 1
-    for m, n, k in ((0, 8, 64), (2, 0, 64), (2, 8, 0), (2, 8, 48), (2, 8, 16), (2, 8, 2**31 + 32)):
+    for m, n, k in ((0, 8, 64), (2, 0, 64), (2, 8, 0), (2, 8, 48), (2, 8, 16), (2, 8, 2**31 + 32),
+                    (2, 2**31 - 2**16 + 1, 64), (2**31 - 2**16 + 1, 8, 64)):
         assert call(_p(x), _p(w, u8p), _p(s), _p(y), m, n, k) == 1
     assert b"k%32" in lib.spaceslug_last_error()
 
