@@ -315,7 +315,7 @@ const char* cq4_problem(const spaceslug_cq4_matrix* w, const void* a, uint32_t m
     if (m == 0 || m > 65535) return "need 1 <= m <= 65535";
     if (w->bits == 0 || w->bits > 4) return "bits must be 1..4";
     if (w->K == 0 || w->N == 0 || w->group_size == 0 || w->num_groups == 0) return "zero dimension";
-    if (w->K > INT32_MAX || w->N > INT32_MAX) return "dimension too large";
+    if (w->K > kMaxRowsCols || w->N > kMaxRowsCols) return "dimension too large (K, N <= 2^31 - 2^16)";
     if (!w->codebook || !w->norms || !w->packed_indices) return "codebook, norms and packed_indices are required";
     const bool orth = (w->flags & SPACESLUG_CQ4_FLAG_ORTHOGONAL) != 0;
     const bool inter = (w->flags & SPACESLUG_CQ4_FLAG_INTERLEAVED_4ROW) != 0;
