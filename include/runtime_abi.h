@@ -243,8 +243,8 @@ void spaceslug_q4_chain_destroy(spaceslug_q4_chain* chain);
  * without writing (null pointers, bits outside 1..4, zero sizes, K != gs * groups)
  * and also for layouts it does not define: a Hadamard group size that is not a
  * power of two up to 256 (its transform buffer holds 256), interleaved panels with
- * bits != 4, N % 4 != 0 or gs % 8 != 0, and M > 65535. `expanded` and `norm_f32`
- * are ignored, as the reference ignores them. */
+ * bits != 4, N % 4 != 0 or gs % 8 != 0, M > 65535, and K or N above 2^31 - 2^16.
+ * `expanded` and `norm_f32` are ignored, as the reference ignores them. */
 #define SPACESLUG_CQ4_FLAG_ORTHOGONAL (1u << 2)
 #define SPACESLUG_CQ4_FLAG_INTERLEAVED_4ROW (1u << 3)
 
