@@ -623,12 +623,14 @@ hipError_t launch_gemv(const DeviceInfo& dev, const float* x, const uint8_t* w_p
         if (groups <= static_cast<uint32_t>(kGemvPipeMaxGroups))
             return launch_gemv_pipelined<2>(dev, x, w_packed, w_scales, y, n, k, stream);
         // Two rows' digits of two groups per lane take 128 registers, so the K-split forms run at
-        // most two wavefronts per SIMD; between K = 8192 and 12288, where four parts of two lane
-        // slots would leave a third of the lanes idle, six parts of one slot (3 per SIMD) instead:
+        // most two wavefronts per SIMD (up to K = 8192 two, against one in the one-row form:
+        // 2 x 8192 -> 14336 20.4 against 22.4 us); between K = 8192 and 12288, where four parts of two
+        // lane slots would leave a third of the lanes idle, six parts of one slot (3 per SIMD) instead:
         // 2 x 11008 -> 8192 20.8 against 23.8 us (one slot at K = 8192 or 14336 is slower: 11.3
-        // against 10.0 and 17.1 against 15.4 us).
+        // against 10.0 and 17.1 against 15.4 us). Up to K = 4096 the one-wavefront kernel beats the
+        // K-split one at two wavefronts per SIMD (2 x 4096 -> 14336: 11.5 against 12.3 us).
         if (groups <= 2u * kGemvPipeMaxGroups)
-            return launch_gemv_split<4, 2, 256, 2>(dev, x, w_packed, w_scales, y, n, k, stream);
+            return launch_gemv_split<4, 2, 512, 2>(dev, x, w_packed, w_scales, y, n, k, stream);
         if (groups <= 3u * kGemvPipeMaxGroups)
             return launch_gemv_split<3, 6, 768, 2, 1>(dev, x, w_packed, w_scales, y, n, k, stream);
         return launch_gemv_split<3, 4, 512, 2>(dev, x, w_packed, w_scales, y, n, k, stream);
