@@ -283,14 +283,15 @@ def test_nan_in_x_gives_nan_outputs(session, oracle, gpu, m, k):
         check(oracle, got[1:], oracle.q4gemm_packed(x[1:], c.packed, c.scales), label="rows without nan")
 
 
-@pytest.mark.parametrize("m,k", [(1, 512), (1, 8192), (1, 14336), (1, 28672), (1, 32800), (2, 4096), (2, 14336),
-                                 (3, 512), (24, 512), (24, 544), (64, 512), (64, 544)])
+@pytest.mark.parametrize("m,k", [(1, 512), (1, 8192), (1, 11008), (1, 14336), (1, 28672), (1, 32800), (2, 2048),
+                                 (2, 4096), (2, 8192), (2, 11008), (2, 14336), (3, 512), (24, 512), (24, 544),
+                                 (64, 512), (64, 544)])
 def test_nonfinite_x_matches_reference_pattern(session, oracle, gpu, m, k):
-    """Infinities and NaNs in x on every path: the integer GEMV (1 x 512), its K-split form
-    (1 x 8192, 1 x 28672, and 1 x 14336 with the infinity in the last group, which only the last
-    of a column's four wavefronts holds), its two-row forms (2 x 4096 and 2 x 14336, with the
-    infinity in the last group; the second row finite: it is then formed by the same IEEE path and
-    meets the usual bar), the small-batch digit kernel
+    """Infinities and NaNs in x on every path: the integer GEMV (1 x 512), its K-split forms
+    (1 x 8192, 11008, 28672, and 1 x 14336 with the infinity in the last group, which only the last
+    of a column's four wavefronts holds), its two-row forms (2 x 2048, 4096, 8192, 11008, and
+    2 x 14336 with the infinity in the last group; the second row finite: it is then formed by the
+    same IEEE path and meets the usual bar), the small-batch digit kernel
     (1 x 32800, 3 and 24 rows), the mid-size bf16-limb kernel (64 x 512) and the wide bf16-limb
     kernel with a K split and its reduction launch (64 x 544: K % 64 != 0 keeps it off the
     mid-size kernel). Every output of a
