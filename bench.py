@@ -29,7 +29,7 @@ least 15 HIP-event-timed iterations after warm-up:
   - "small_batch" (M=16, K=N=4096, 32 weight copies per step) and "lora" (M=512, K=N=4096, rank 16);
   - "decode_down": one row through the transposed shape, K=14336, N=4096 (the MLP's down projection;
     64 weight copies per step, the same 36.7 MB per call as the headline), which takes the K-split
-    form of the decode GEMV;
+    form of the decode GEMV; timed call by call and, as "hip_graph", as one replayed graph per step;
   - "reference_bench": the reference's own q4gemm benchmark configuration (bench_q4gemm.cpp: M=N=K=1024,
     its LCG generators and seeds, 128 warm-ups, median of 15 timed calls, TFLOP/s = 2*N^3 / time);
   - "cq4": the CQ4 codebook matmul on the reference's CQ4 benchmark shapes;
@@ -326,9 +326,11 @@ def bench_gemv(torch, session, steps: int, warmup: int, copies: int = 64, launch
 
 
 def bench_gemm(torch, session, m: int, n: int, k: int, copies: int, iters: int, warmup: int, rank: int = 0,
-               inputs: dict | None = None) -> dict:
+               inputs: dict | None = None, graph: bool = False) -> dict:
     """One step = `copies` calls over distinct weight copies; each step timed on its own, median reported.
-    The GPU output of the first call (weight copy 0) is kept with its inputs for the parity check."""
+    The GPU output of the first call (weight copy 0) is kept with its inputs for the parity check. With
+    `graph`, the step is also captured once as a HIP graph and its replay timed the same way (as the
+    headline GEMV's sweep is), reported beside the call-by-call figure."""
     gen = torch.Generator(device="cuda").manual_seed(99)
     if inputs is None:
         packed, scales = make_weights(torch, n, k, copies, gen)
@@ -366,7 +368,16 @@ def bench_gemm(torch, session, m: int, n: int, k: int, copies: int, iters: int, 
     per_call = t["median"] * 1e-3 / copies
     fl = algo_flops(m, n, k, rank)
     by = algo_bytes(m, n, k, rank)
-    return {"m": m, "n": n, "k": k, "rank": rank, "copies": copies, "ms_per_call": per_call * 1e3,
+    replay = None
+    if graph:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step()
+        tg = time_each(torch, g.replay, iters, warmup)
+        replay = {"us_per_call": round(tg["median"] * 1e3 / copies, 3),
+                  "gbs": round(by / (tg["median"] * 1e-3 / copies) / 1e9, 2)}
+        del g
+    return {"m": m, "n": n, "k": k, "rank": rank, "copies": copies, "ms_per_call": per_call * 1e3, "graph": replay,
             "min_ms_per_call": t["min"] / copies, "max_ms_per_call": t["max"] / copies, "iters": t["iters"],
             "tflops": fl / per_call / 1e12, "gbs": by / per_call / 1e9, "flops_per_call": fl, "bytes_per_call": by,
             "host_us_per_call": t["host_us_per_call"] / copies,
@@ -809,10 +820,11 @@ def main() -> int:
         result["small_batch"] = gemm_entry(sb, unit_gbs=True)
         torch.cuda.empty_cache()
         print("[bench] decode down projection 1x14336->4096 x64 copies", file=sys.stderr, flush=True)
-        dd = bench_gemm(torch, session, 1, 4096, 14336, copies=64, iters=iters, warmup=3)
+        dd = bench_gemm(torch, session, 1, 4096, 14336, copies=64, iters=iters, warmup=3, graph=True)
         checks["decode_down"] = dd.pop("check")
         result["decode_down"] = gemm_entry(dd, unit_gbs=True)
-        result["decode_down"]["hbm_frac"] = round(dd["gbs"] / 8000.0, 4)
+        result["decode_down"]["hbm_frac"] = round(dd["gbs"] / HBM_PEAK_GBS, 4)
+        result["decode_down"]["hip_graph"] = dd["graph"]
         torch.cuda.empty_cache()
         print("[bench] lora 512x4096x4096 r16", file=sys.stderr, flush=True)
         lo = bench_gemm(torch, session, 512, 4096, 4096, copies=1, iters=iters, warmup=3, rank=16)
